@@ -1,0 +1,133 @@
+/*
+ * vllm_exact_amd.h -- C ABI of the MI355X (gfx950) exact linear path.
+ *
+ * One shared library, libvllm_exact_amd.so, built from the HIP sources in vllm-exact_amd/csrc.
+ * Every entry point:
+ *   - takes device pointers, 64-bit sizes and element strides (innermost dimension
+ *     contiguous), element-type enums and a hipStream_t passed as `vxa_stream_t`;
+ *   - never allocates, never synchronises, never reads device memory on the host;
+ *   - launches asynchronously on `stream` and returns a VXA_* status code.
+ * Workspace (split-K partial sums, attention segment partials) is owned by the caller;
+ * its size comes from the matching *_plan / *_workspace query.
+ *
+ * The Python layer (vllm_exact.kernels / vllm_exact.paged_attn) binds these with ctypes
+ * and keeps the reference's Python surface on top of them.
+ */
+#ifndef VLLM_EXACT_AMD_H
+#define VLLM_EXACT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The Python binding maps ERR_ARG to ValueError, ERR_UNSUPPORTED to
+ * NotImplementedError (so autotune/tuners can skip a config, kernels.py:313-314), and the
+ * rest to RuntimeError. */
+enum {
+  VXA_OK = 0,
+  VXA_ERR_ARG = 1,          /* bad pointer / size / stride / F / dtype */
+  VXA_ERR_UNSUPPORTED = 2,  /* shape or config outside what the kernels implement */
+  VXA_ERR_WORKSPACE = 3,    /* workspace missing or smaller than the plan requires */
+  VXA_ERR_LAUNCH = 4        /* hipLaunchKernel / hipGetLastError failure */
+};
+
+/* Element types of floating-point tensors crossing the boundary. */
+enum { VXA_F32 = 0, VXA_BF16 = 1, VXA_F16 = 2 };
+
+typedef void* vxa_stream_t; /* a hipStream_t; NULL is the null stream */
+
+/* Library version string and a human-readable status message. */
+const char* vxa_version(void);
+const char* vxa_status_string(int status);
+
+/*
+ * Per-row F-bit fixed-point digitization.
+ * Replaces kernels.py:74-85 (`digitize`, device body `_digitize_kernel` kernels.py:47-71;
+ * numerical spec kernels.py:3-9, CPU statement `digitize_torch` kernels.py:22-39).
+ *   x       [rows, k] with row stride ldx (elements), dtype VXA_F32 / VXA_BF16 / VXA_F16
+ *   h, l    int8 [rows, k] digit planes, row stride ldd (bytes == elements)
+ *   cs      int32 [rows] row sum of 256*h+l (F == 15), 0 otherwise
+ *   sh      int32 [rows] shift: q = trunc(x * 2^sh)
+ *   f       fixed-point bits, 1..15; f == 15 uses offset digits, f < 15 balanced digits
+ */
+int vxa_digitize(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                 int8_t* h, int8_t* l, int64_t ldd, int32_t* cs, int32_t* sh,
+                 int f, vxa_stream_t stream);
+
+/*
+ * Split-K plan for vxa_exact_linear. Replaces the host arithmetic of kernels.py:268-273:
+ * KCH = cdiv(cdiv(K, SK), BK) * BK, SK = cdiv(K, KCH), workspace int64 [SK, M, N] when SK > 1.
+ *   cfg, cfg_len  the reference cfg tuple (BM, BN, BK, warps, stages, GM[, SK[, mma]]),
+ *                 cfg_len in 6..8 (kernels.py:268-270); mma is accepted and ignored
+ *                 (INT8 MFMA gives the same bits).
+ *   *sk_out       number of K splits actually used
+ *   *kch_out      K extent of one split
+ *   *ws_bytes     workspace bytes the caller must pass to vxa_exact_linear (0 if none)
+ */
+int vxa_exact_linear_plan(int64_t m, int64_t n, int64_t k, const int32_t* cfg, int cfg_len,
+                          int32_t* sk_out, int64_t* kch_out, size_t* ws_bytes);
+
+/*
+ * Exact two-digit linear layer: out[m, n] = round(2^-(sx[m]+sw[n]) * tot[m, n]) with
+ *   tot = 2^16 * sum(xh*wh) + 2^8 * sum(xh*wl + xl*wh) [+ sum(xl*wl) unless trunc]
+ *         [+ 128*(cx[m] + cw[n]) + 128*128*K when f == 15]
+ * accumulated exactly (int8 MFMA -> int32 -> int64), converted int64 -> fp64 (exact)
+ * -> fp32 (RNE) -> out dtype (RNE). Replaces kernels.py:257-289 (`exact_linear`), with the
+ * device bodies `_exact_kernel` kernels.py:104-157 and `_exact_fin` kernels.py:159-177.
+ *   xh, xl [m, k] int8 row stride ldx; cx, sx int32 [m]      (activation digits)
+ *   wh, wl [n, k] int8 row stride ldw; cw, sw int32 [n]      (weight digits, NT layout)
+ *   out    [m, n] row stride ldo, dtype VXA_F32 / VXA_BF16 / VXA_F16
+ *   ws     int64 workspace of at least the planned ws_bytes (may be NULL if 0)
+ * Bits do not depend on cfg: every tiling and split-K partition gives the same output.
+ */
+int vxa_exact_linear(const int8_t* xh, const int8_t* xl, const int32_t* cx, const int32_t* sx,
+                     int64_t ldx,
+                     const int8_t* wh, const int8_t* wl, const int32_t* cw, const int32_t* sw,
+                     int64_t ldw,
+                     void* out, int out_dtype, int64_t ldo,
+                     int64_t m, int64_t n, int64_t k, int f, int trunc,
+                     const int32_t* cfg, int cfg_len,
+                     void* ws, size_t ws_bytes, vxa_stream_t stream);
+
+/*
+ * Workspace bytes for vxa_paged_decode: fp32 segment partials m, l [n, H, NS] and
+ * acc [n, H, NS, D] with NS = max(1, cdiv(max_len, split)) (paged_attn.py:105-108).
+ * Zero when NS == 1 (every request then finishes inside one segment).
+ */
+int vxa_paged_decode_workspace(int64_t n, int64_t num_heads, int64_t head_dim, int64_t max_len,
+                               int64_t split, size_t* ws_bytes);
+
+/*
+ * Paged decode attention for one new token per request, with a fixed reduction order.
+ * Replaces paged_attn.py:97-114 (`paged_decode`, device bodies `_paged_partial`
+ * paged_attn.py:31-72 and `_paged_merge` paged_attn.py:75-94).
+ *   q        bf16 [>=n, H, D], strides (sqt, sqh) in elements, innermost contiguous
+ *   k_cache, v_cache  bf16 views (num_blocks, block_size, KV, D) with element strides
+ *            (skb, skp, skh) and (svb, svp, svh); innermost contiguous
+ *            (vLLM FlashAttention layout, paged_attn.py:8-9)
+ *   block_table int32 [B, max_blocks] row stride sbt; seq_lens int32 [B]
+ *   scale    softmax scale
+ *   out      [>=n, H, D] strides (sot, soh), dtype VXA_F32 / VXA_BF16 / VXA_F16
+ *   n        number of leading requests to compute (paged_attn.py:99)
+ *   max_len  model maximum length: fixes NS = cdiv(max_len, split) (paged_attn.py:105)
+ *   split    keys per segment; blk keys per online-softmax step (16, 32 or 64);
+ *            waves per workgroup (4 or 8). split, blk and waves fix the floating-point
+ *            order; the result never depends on n or on the other requests.
+ */
+int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh,
+                     const void* k_cache, int64_t skb, int64_t skp, int64_t skh,
+                     const void* v_cache, int64_t svb, int64_t svp, int64_t svh,
+                     const int32_t* block_table, int64_t sbt, const int32_t* seq_lens,
+                     float scale, void* out, int out_dtype, int64_t sot, int64_t soh,
+                     int64_t n, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                     int64_t block_size, int64_t max_len, int64_t split, int64_t blk,
+                     int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_EXACT_AMD_H */

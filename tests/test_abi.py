@@ -1,0 +1,108 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/*.h declares, and
+its host-only entry points (plans, workspace sizes, argument validation) behave as
+documented. No kernel is launched here."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from vllm_exact import _native as nx
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    names = set()
+    for hdr in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(vxa_\w+)\s*\(", text))
+    return names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    assert nx.available(), "build the HIP library first (make -C vllm-exact_amd)"
+    lib = ctypes.CDLL(str(nx.LIB_PATH))
+    declared = declared_functions()
+    assert declared == set(nx.EXPORTED), declared ^ set(nx.EXPORTED)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_status_strings():
+    assert "gfx950" in nx.version()
+    L = nx.lib()
+    assert L.vxa_status_string(nx.VXA_OK) == b"ok"
+    assert b"workspace" in L.vxa_status_string(nx.VXA_ERR_WORKSPACE)
+
+
+def _plan(M, N, K, cfg):
+    return nx.exact_plan(M, N, K, cfg)
+
+
+def test_split_k_plan_follows_reference_arithmetic():
+    # kernels.py:271-272: KCH = cdiv(cdiv(K, SK), BK) * BK, SK = cdiv(K, KCH)
+    assert _plan(16, 4096, 4096, (16, 64, 128, 4, 3, 8, 1)) == (1, 4096, 0)
+    assert _plan(16, 4096, 4096, (16, 64, 128, 4, 3, 8, 4)) == (4, 1024, 4 * 16 * 4096 * 8)
+    assert _plan(5, 200, 12288, (16, 128, 256, 8, 3, 8, 8)) == (8, 1536, 8 * 5 * 200 * 8)
+    # K = 4096 split 8 ways with BK = 256 -> KCH = 512
+    assert _plan(1, 64, 4096, (16, 64, 256, 4, 3, 8, 8))[:2] == (8, 512)
+    # uneven: K = 1000, SK = 3, BK = 128 -> KCH = 384, SK = 3
+    assert _plan(2, 64, 1000, (16, 64, 128, 4, 3, 8, 3))[:2] == (3, 384)
+    # BK below one MFMA step (64) rounds chunks up to 64
+    assert _plan(2, 64, 4096, (16, 64, 32, 4, 3, 8, 8))[:2] == (8, 512)
+    # a single int32 accumulator never spans more than 32768 terms
+    sk, kch, _ = _plan(1, 64, 65536, (16, 64, 128, 4, 3, 8, 1))
+    assert kch <= 32768 and sk * kch >= 65536
+    # mma (8th field) is accepted and does not change the plan
+    assert _plan(24, 384, 4096, (64, 128, 128, 4, 4, 8, 2, 1)) == _plan(24, 384, 4096, (64, 128, 128, 4, 4, 8, 2, 0))
+
+
+def test_plan_rejects_bad_cfgs():
+    with pytest.raises(ValueError):
+        nx.cfg_array((16, 64, 128, 4, 3))
+    with pytest.raises(ValueError):
+        _plan(1, 64, 4096, (0, 64, 128, 4, 3, 8))
+    with pytest.raises(ValueError):
+        _plan(-1, 64, 4096, (16, 64, 128, 4, 3, 8))
+
+
+def test_paged_workspace_sizes():
+    # paged_attn.py:105-108: NS = max(1, cdiv(MAX_LEN, split)); partials only when NS > 1
+    assert nx.paged_workspace(64, 32, 128, 1024, 1024) == 0
+    assert nx.paged_workspace(64, 32, 128, 16784, 1024) == 64 * 32 * 17 * 130 * 4
+    assert nx.paged_workspace(4, 16, 256, 9000, 4096) == 4 * 16 * 3 * 258 * 4
+
+
+def test_entry_points_validate_before_launching():
+    L = nx.lib()
+    # digitize: F outside 1..15 and negative sizes are argument errors; zero rows is a no-op
+    assert L.vxa_digitize(None, nx.VXA_F32, 4, 64, 64, None, None, 64, None, None, 16, None) == nx.VXA_ERR_ARG
+    assert L.vxa_digitize(None, nx.VXA_F32, -1, 64, 64, None, None, 64, None, None, 14, None) == nx.VXA_ERR_ARG
+    assert L.vxa_digitize(None, nx.VXA_F32, 0, 64, 64, None, None, 64, None, None, 14, None) == nx.VXA_OK
+    assert L.vxa_digitize(None, 7, 4, 64, 64, None, None, 64, None, None, 14, None) == nx.VXA_ERR_ARG
+    arr, n = nx.cfg_array((16, 64, 128, 4, 3, 8, 4))
+    # exact_linear: an empty output is a no-op; missing workspace for split-K is reported
+    assert L.vxa_exact_linear(None, None, None, None, 64, None, None, None, None, 64, None, nx.VXA_F32, 64,
+                              0, 64, 64, 14, 1, arr, n, None, 0, None) == nx.VXA_OK
+    fake = 16  # never dereferenced: validation fails first
+    assert L.vxa_exact_linear(fake, fake, fake, fake, 4096, fake, fake, fake, fake, 4096, fake, nx.VXA_F32, 4096,
+                              16, 4096, 4096, 14, 1, arr, n, None, 0, None) == nx.VXA_ERR_WORKSPACE
+    assert L.vxa_exact_linear(fake, fake, fake, fake, 4096, fake, fake, fake, fake, 4096, fake, 9, 4096,
+                              16, 4096, 4096, 14, 1, arr, n, None, 0, None) == nx.VXA_ERR_ARG
+    # paged decode: unsupported head size / group / split are reported as unsupported
+    args = dict(q=fake, sqt=4096, sqh=128, kc=fake, skb=4096, skp=2048, skh=256, vc=fake, svb=4096, svp=2048,
+                svh=256, bt=fake, sbt=8, sl=fake, scale=0.1, out=fake, od=nx.VXA_BF16, sot=4096, soh=128, n=2,
+                H=32, KV=8, D=128, BS=16, max_len=1024, split=1024, blk=64, waves=4, ws=None, wsb=0, st=None)
+
+    def call(**over):
+        a = dict(args, **over)
+        return L.vxa_paged_decode(*a.values())
+
+    assert call(D=96) == nx.VXA_ERR_UNSUPPORTED
+    assert call(H=24, KV=8) == nx.VXA_ERR_UNSUPPORTED  # G = 3
+    assert call(split=1000) == nx.VXA_ERR_UNSUPPORTED
+    assert call(blk=48) == nx.VXA_ERR_UNSUPPORTED
+    assert call(H=30, KV=8) == nx.VXA_ERR_ARG
+    assert call(max_len=4096) == nx.VXA_ERR_WORKSPACE
+    assert call(n=0) == nx.VXA_OK

@@ -1,0 +1,106 @@
+"""CPU checks of the host-side mirror of the reference interface: config tables and bucket
+lookup (plugin.py:27-48), the custom op's registration, enable()'s guards
+(__init__.py:44-47), the CPU-tensor policy of the GPU entry points, and the torch
+statements (*_torch) against the oracle."""
+import json
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import vllm_exact
+from helpers import make_paged, xw
+from vllm_exact import kernels as K
+from vllm_exact import paged_attn as P
+from vllm_exact import plugin
+
+
+def test_table_bucket_lookup(tmp_path):
+    table = {"4096,4096": {"1": [16, 64, 128, 4, 1, 8, 4], "16": [16, 128, 128, 8, 1, 8, 2],
+                           "64": [64, 64, 128, 4, 1, 8, 1, 0]}}
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(table))
+    plugin.load_table(path)
+    try:
+        assert plugin._cfg(1, 4096, 4096) == (16, 64, 128, 4, 1, 8, 4)
+        assert plugin._cfg(2, 4096, 4096) == (16, 128, 128, 8, 1, 8, 2)  # smallest tuned M >= M
+        assert plugin._cfg(16, 4096, 4096) == (16, 128, 128, 8, 1, 8, 2)
+        assert plugin._cfg(17, 4096, 4096) == (64, 64, 128, 4, 1, 8, 1, 0)
+        assert plugin._cfg(300, 4096, 4096) == (64, 64, 128, 4, 1, 8, 1)  # beyond: last row, SK = 1
+        assert plugin._cfg(16, 6144, 4096) == plugin.DEFAULT_CFGS[0][1]  # shape not in the table
+    finally:
+        plugin.load_table(None)
+    assert plugin._cfg(1, 4096, 4096) == plugin.DEFAULT_CFGS[0][1]
+    assert plugin._cfg(4096, 4096, 4096) == plugin.LARGE_M_CFG
+
+
+def test_shipped_table_is_well_formed():
+    path = vllm_exact.TABLES["mi355x"]
+    raw = json.loads(path.read_text())
+    for nk, row in raw.items():
+        n, k = map(int, nk.split(","))
+        assert n > 0 and k > 0
+        for m, cfg in row.items():
+            assert int(m) > 0 and 7 <= len(cfg) <= 8
+    plugin.load_table(path)
+    plugin.load_table(None)
+
+
+def test_custom_op_is_registered_with_fake():
+    op = torch.ops.exactmm.linear
+    x = torch.empty(3, 5, 64, device="meta", dtype=torch.bfloat16)
+    wh = torch.empty(96, 64, device="meta", dtype=torch.int8)
+    cw = torch.empty(96, device="meta", dtype=torch.int32)
+    y = op(x, wh, wh, cw, cw)
+    assert y.shape == (3, 5, 96) and y.dtype == torch.bfloat16
+
+
+def test_gpu_entry_points_refuse_cpu_tensors():
+    x, w = xw(4, 8, 128)
+    with pytest.raises(ValueError, match="digitize_torch"):
+        K.digitize(x, 14)
+    xd, wd = K.digitize_torch(x, 14), K.digitize_torch(w, 14)
+    with pytest.raises(ValueError, match="exact_linear_torch"):
+        K.exact_linear(xd, wd, 14, True)
+    q, kv, bt, sl = make_paged(2, 40, 16, 4, 1, 64)
+    kc, vc = kv.transpose(1, 2).split(64, dim=-1)
+    with pytest.raises(ValueError, match="paged_decode_torch"):
+        P.paged_decode(q, kc, vc, bt, sl, 0.125, torch.empty(2, 4, 64), 2, 40)
+
+
+def test_enable_guards(monkeypatch):
+    monkeypatch.setattr(vllm_exact, "_ENABLED", True)
+    with pytest.raises(RuntimeError, match="only be called once"):
+        vllm_exact.enable(1024)
+    monkeypatch.setattr(vllm_exact, "_ENABLED", False)
+    monkeypatch.setitem(sys.modules, "vllm", object())
+    with pytest.raises(RuntimeError, match="before importing vllm"):
+        vllm_exact.enable(1024)
+    monkeypatch.delitem(sys.modules, "vllm")
+    with pytest.raises(ValueError, match="another GPU"):
+        vllm_exact.enable(1024, cfg_table="h200")
+    if not plugin.HAVE_VLLM:
+        with pytest.raises(ImportError):
+            vllm_exact.enable(1024)
+    assert vllm_exact._ENABLED is False
+
+
+@pytest.mark.parametrize("F,trunc", [(14, True), (14, False), (15, False)])
+def test_torch_statements_match_oracle(F, trunc):
+    x, w = xw(9, 70, 1024, seed=5)
+    xd, wd = K.digitize_torch(x, F), K.digitize_torch(w, F)
+    y = K.exact_linear_torch(xd, wd, F, trunc).numpy()
+    want = oracle.exact_linear_c(tuple(t.numpy() for t in xd), tuple(t.numpy() for t in wd), F, trunc)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    assert K.digitize_weight(w.to(torch.bfloat16), F)[3].dtype == torch.int32
+
+
+def test_paged_decode_torch_matches_oracle():
+    q, kv, bt, sl = make_paged(3, 100, 16, 8, 2, 64, seed=4)
+    kc, vc = kv.transpose(1, 2).split(64, dim=-1)
+    got = P.paged_decode_torch(q, kc, vc, bt, sl, 0.125, 3).double().numpy()
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    want = oracle.paged_decode_c(bits(q), bits(kc), bits(vc), bt.numpy(), sl.numpy(), 0.125, 3)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)

@@ -1,0 +1,56 @@
+// Shared device helpers for the gfx950 exact linear path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/vllm_exact_amd.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef unsigned short v8u16 __attribute__((ext_vector_type(8)));
+
+template <typename T>
+__host__ __device__ inline constexpr T cdiv(T a, T b) {
+  return (a + b - 1) / b;
+}
+
+// bf16 bit pattern -> fp32 (exact).
+__device__ inline float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16 with round-to-nearest-even; NaN -> 0x7FC0 (the canonical quiet NaN torch
+// produces). Infinities and overflow follow IEEE (the rounding bias carries into the
+// exponent and saturates at the Inf pattern).
+__device__ inline uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Store one fp32 value to an output of runtime dtype (uniform branch across the wave).
+__device__ inline void store_f32_as(void* out, int dtype, int64_t idx, float v) {
+  if (dtype == VXA_F32) {
+    reinterpret_cast<float*>(out)[idx] = v;
+  } else if (dtype == VXA_BF16) {
+    reinterpret_cast<uint16_t*>(out)[idx] = f32_to_bf16_rne(v);
+  } else {
+    reinterpret_cast<_Float16*>(out)[idx] = (_Float16)v;  // v_cvt_f16_f32: RNE
+  }
+}
+
+// Wave-wide lane shuffles built on ds_bpermute (byte-addressed lane index).
+__device__ inline float shfl_f32(float v, int src_lane) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(v)));
+}
+__device__ inline float shfl_xor_f32(float v, int mask) {
+  const int lane = threadIdx.x & 63;
+  return shfl_f32(v, lane ^ mask);
+}
+
+#define VXA_CHECK_LAUNCH()                         \
+  do {                                             \
+    if (hipGetLastError() != hipSuccess) return VXA_ERR_LAUNCH; \
+  } while (0)

@@ -1,0 +1,209 @@
+"""Exact INT8 two-digit linear layers on MI355X: digitization and exact matmul.
+
+Numerical spec (the reference's kernels.py:3-9):
+- activations and weights are converted per row to F-bit fixed point with one power-of-two
+  scale per row and split into two INT8 digits, q = 256*h + l. F = 15 uses offset digits
+  with a row-sum correction; F < 15 uses balanced digits. trunc=True drops the l*l term.
+- digit products are exact on INT8 matrix cores and accumulate in int32 then int64, so the
+  result does not depend on tiling, split-K partition, batch size or the other rows.
+  int64 -> fp64 is exact, fp64 -> fp32 rounds once, fp32 -> bf16/fp16 rounds once more.
+
+Entry points keep the reference's names and signatures (kernels.py:22-43, 74-100, 250-316):
+digitize_torch, digitize_weight, digitize, exact_linear_torch, exact_linear,
+autotune_exact, EXACT_CFGS. `digitize` and `exact_linear` run the gfx950 HIP kernels of
+libvllm_exact_amd.so and accept only GPU tensors; the *_torch functions are the plain
+torch statements of the same integer arithmetic (the reference's CPU path).
+"""
+import torch
+
+from . import _native as _nx
+
+HAVE_HIP = _nx.available() and torch.cuda.is_available()
+HAVE_TRITON = False  # the reference's backend flag (kernels.py:13-18); this build has no Triton path
+
+
+# ======================= fixed-point digitization =======================
+def digitize_torch(x, F):
+    """(R, K) float -> (h int8, l int8, cs int32, sh int32) in plain torch (kernels.py:22-39).
+
+    e is the frexp exponent of the row absmax (0 for a zero row), sh = F - e, 2^sh is built
+    from its fp32 bit pattern, and q = trunc(x * 2^sh) (the float -> int cast truncates).
+    """
+    x = x.float()
+    amax = x.abs().amax(dim=1)
+    e = torch.frexp(amax).exponent
+    e = torch.where(amax > 0, e, torch.zeros_like(e)).to(torch.int32)
+    sh = (F - e).to(torch.int32)
+    two_sh = ((sh + 127) << 23).view(torch.float32)
+    q = (x * two_sh.unsqueeze(1)).to(torch.int32)
+    if F == 15:
+        lo = (q & 255) - 128
+        hi = (q - lo - 128) >> 8
+        cs = (256 * hi + lo).sum(dim=1, dtype=torch.int32)
+    else:
+        lo = ((q + 128) & 255) - 128
+        hi = (q - lo) >> 8
+        cs = torch.zeros_like(sh)
+    return hi.to(torch.int8), lo.to(torch.int8), cs.to(torch.int32), sh
+
+
+def digitize_weight(w, F):
+    return digitize_torch(w.float(), F)
+
+
+def _require_gpu(t, what):
+    if not t.is_cuda:
+        raise ValueError(
+            f"{what} runs the gfx950 HIP kernels and needs GPU tensors; "
+            f"use {what}_torch for the CPU statement of the same arithmetic")
+    _nx.lib()  # raises if the HIP library is missing
+
+
+def digitize(x, F, out=None):
+    """Digitize the rows of a GPU tensor x (R, K) (fp32, bf16 or fp16) with the HIP kernel.
+
+    Returns (h, l, cs, sh) like digitize_torch; bf16 input gives the same digits as its fp32
+    upcast (kernels.py:74-85)."""
+    _require_gpu(x, "digitize")
+    if x.dim() != 2:
+        raise ValueError(f"digitize expects a 2-D tensor, got shape {tuple(x.shape)}")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    R, K = x.shape
+    dev = x.device
+    if out is None:
+        out = (torch.empty((R, K), dtype=torch.int8, device=dev), torch.empty((R, K), dtype=torch.int8, device=dev),
+               torch.empty(R, dtype=torch.int32, device=dev), torch.empty(R, dtype=torch.int32, device=dev))
+    h, l, cs, sh = out
+    if h.shape != (R, K) or l.shape != (R, K) or h.dtype != torch.int8 or l.dtype != torch.int8:
+        raise ValueError("digitize: h/l must be int8 tensors of shape (R, K)")
+    if h.stride(1) != 1 or l.stride(1) != 1 or h.stride(0) != l.stride(0):
+        raise ValueError("digitize: h/l must be row-major with equal row strides")
+    if cs.numel() != R or sh.numel() != R or cs.dtype != torch.int32 or sh.dtype != torch.int32:
+        raise ValueError("digitize: cs/sh must be int32 tensors of R elements")
+    if not (cs.is_contiguous() and sh.is_contiguous()):
+        raise ValueError("digitize: cs/sh must be contiguous")
+    with torch.cuda.device(dev):
+        st = _nx.stream_handle(dev)
+        _nx.check(_nx.lib().vxa_digitize(x.data_ptr(), _nx.dtype_enum(x.dtype), R, K, x.stride(0), h.data_ptr(),
+                                         l.data_ptr(), h.stride(0), cs.data_ptr(), sh.data_ptr(), F, st),
+                  "digitize")
+    return out
+
+
+# ======================= exact linear layer =======================
+def exact_linear_torch(xd, wd, F, trunc=False):
+    """Integer closed form in torch int64 (kernels.py:89-100); returns fp32 (M, N)."""
+    xh, xl, cx, sx = (t.long() for t in xd)
+    wh, wl, cw, sw = (t.long() for t in wd)
+    K = xh.shape[1]
+    tot = (xh @ wh.T) * 65536 + (xh @ wl.T + xl @ wh.T) * 256
+    if not trunc:
+        tot = tot + xl @ wl.T
+    if F == 15:
+        tot = tot + 128 * (cx[:, None] + cw[None, :]) + 128 * 128 * K
+    e = -(sx[:, None] + sw[None, :])
+    two_e = ((e + 1023) << 52).view(torch.float64)
+    return (tot.double() * two_e).float()
+
+
+# gfx950 candidates (BM, BN, BK, waves, stages, GM): BM picks 16/32/64-row blocks, BN the
+# workgroup's 64/128/256 output columns, waves the workgroup size (waves share N first,
+# then K). BK only rounds split-K chunks; stages and GM are accepted for the reference's
+# format and do not change the gfx950 schedule.
+EXACT_CFGS = [(16, 64, 128, 4, 1, 8), (16, 64, 128, 8, 1, 8), (16, 128, 128, 4, 1, 8), (16, 128, 128, 8, 1, 8),
+              (16, 256, 128, 4, 1, 8), (16, 256, 128, 8, 1, 8), (32, 64, 128, 4, 1, 8), (32, 64, 128, 8, 1, 8),
+              (32, 128, 128, 4, 1, 8), (32, 128, 128, 8, 1, 8), (64, 64, 128, 4, 1, 8)]
+AUTOTUNE_SPLITS = (1, 2, 4, 8)
+_CFG_CACHE = {}
+
+
+def _check_digits(name, d, rows, K):
+    h, l, c, s = d
+    if h.dtype != torch.int8 or l.dtype != torch.int8 or c.dtype != torch.int32 or s.dtype != torch.int32:
+        raise ValueError(f"exact_linear: {name} digits must be (int8, int8, int32, int32)")
+    if h.shape != (rows, K) or l.shape != (rows, K) or c.numel() != rows or s.numel() != rows:
+        raise ValueError(f"exact_linear: {name} digit shapes disagree")
+    if h.stride(1) != 1 or l.stride(1) != 1 or h.stride(0) != l.stride(0):
+        raise ValueError(f"exact_linear: {name} digit planes must be row-major with equal row strides")
+    if not (c.is_contiguous() and s.is_contiguous()):
+        raise ValueError(f"exact_linear: {name} cs/sh must be contiguous")
+
+
+def exact_linear(xd, wd, F, trunc=False, out=None, cfg=None):
+    """Exact two-digit matmul of digitized x (M, K) and w (N, K) on the HIP kernels.
+
+    out: optional (M, N) fp32/bf16/fp16 GPU tensor (default fp32). cfg: the reference's tuple
+    (BM, BN, BK, warps, stages, GM[, SK[, mma]]); it changes speed only, never bits
+    (kernels.py:257-289). Without cfg the cached or autotuned config is used."""
+    xh, xl, cx, sx = xd
+    wh, wl, cw, sw = wd
+    _require_gpu(xh, "exact_linear")
+    M, K = xh.shape
+    N = wh.shape[0]
+    if wh.shape[1] != K:
+        raise ValueError(f"exact_linear: K mismatch, x has {K}, w has {wh.shape[1]}")
+    _check_digits("x", xd, M, K)
+    _check_digits("w", wd, N, K)
+    dev = xh.device
+    for t in (*xd, *wd):
+        if t.device != dev:
+            raise ValueError("exact_linear: all digit tensors must be on one device")
+    if out is None:
+        out = torch.empty((M, N), device=dev, dtype=torch.float32)
+    if out.shape != (M, N) or out.stride(1) != 1 or out.device != dev:
+        raise ValueError("exact_linear: out must be an (M, N) row-major tensor on the digits' device")
+    key = (M, N, K, F, bool(trunc))
+    cfg = tuple(cfg or _CFG_CACHE.get(key) or autotune_exact(xd, wd, F, trunc))
+    _, _, ws_bytes = _nx.exact_plan(M, N, K, cfg)
+    ws = torch.empty(ws_bytes // 8, dtype=torch.int64, device=dev) if ws_bytes else None
+    arr, n = _nx.cfg_array(cfg)
+    with torch.cuda.device(dev):
+        st = _nx.stream_handle(dev)
+        _nx.check(_nx.lib().vxa_exact_linear(
+            xh.data_ptr(), xl.data_ptr(), cx.data_ptr(), sx.data_ptr(), xh.stride(0),
+            wh.data_ptr(), wl.data_ptr(), cw.data_ptr(), sw.data_ptr(), wh.stride(0),
+            out.data_ptr(), _nx.dtype_enum(out.dtype), out.stride(0), M, N, K, int(F), int(bool(trunc)),
+            arr, n, _nx.ptr(ws), ws_bytes, st), "exact_linear")
+    return out
+
+
+def _next_pow2(v):
+    return 1 << max(0, (int(v) - 1).bit_length())
+
+
+def autotune_exact(xd, wd, F, trunc):
+    """Time every candidate (and split-K factor) with HIP events and cache the fastest
+    (kernels.py:292-316). Candidates the kernels reject are skipped."""
+    M, K = xd[0].shape
+    N = wd[0].shape[0]
+    key = (M, N, K, F, bool(trunc))
+    best = None
+    for c in EXACT_CFGS:
+        if c[0] > max(16, _next_pow2(M)):
+            continue
+        for sk in AUTOTUNE_SPLITS:
+            cand = tuple(c) + (sk,)
+            try:
+                fn = lambda: exact_linear(xd, wd, F, trunc, cfg=cand)
+                fn()
+                torch.cuda.synchronize()
+                st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                st.record()
+                for _ in range(10):
+                    fn()
+                en.record()
+                torch.cuda.synchronize()
+                t = st.elapsed_time(en)
+            except (NotImplementedError, ValueError, RuntimeError):
+                continue
+            if best is None or t < best[0]:
+                best = (t, cand)
+    if best is None:
+        raise RuntimeError(f"autotune_exact: no candidate config ran for M={M} N={N} K={K}")
+    _CFG_CACHE[key] = best[1]
+    return best[1]
+
+
+__all__ = ["HAVE_HIP", "HAVE_TRITON", "digitize_torch", "digitize_weight", "digitize", "exact_linear_torch",
+           "exact_linear", "autotune_exact", "EXACT_CFGS"]

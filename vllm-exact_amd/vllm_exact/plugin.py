@@ -1,0 +1,154 @@
+"""vLLM quantization plugin quantization="exact_int8" (plugin.py of the reference).
+
+Every linear layer (optionally lm_head) goes through the exact two-digit matmul. The
+pieces that do not need vLLM (tuning-table lookup, the `exactmm::linear` custom op, weight
+digitization) are always defined; the vLLM classes are defined when vLLM is importable.
+Globals F, TRUNC, LMHEAD, RB are set by vllm_exact.enable().
+"""
+import json
+from pathlib import Path
+
+import torch
+
+from . import kernels as K
+
+try:  # vLLM is the host engine; it is not needed for the op itself
+    from vllm.model_executor.layers.linear import LinearBase, UnquantizedLinearMethod
+    from vllm.model_executor.layers.quantization import register_quantization_config
+    from vllm.model_executor.layers.quantization.base_config import QuantizationConfig
+    from vllm.model_executor.layers.vocab_parallel_embedding import ParallelLMHead, UnquantizedEmbeddingMethod
+    HAVE_VLLM = True
+except ImportError:
+    HAVE_VLLM = False
+
+# set by enable()
+F = 14
+TRUNC = True
+LMHEAD = True
+_TABLE = None
+RB = 16384  # rows per block: rows are independent, so blocking bounds temporaries without changing bits
+WEIGHT_RB = 32768  # weight rows digitized per block at load time (plugin.py:74)
+
+
+def load_table(path):
+    """Tuning table {"N,K": {"M": [BM, BN, BK, warps, stages, GM, SK(, mma)]}} (plugin.py:27-34).
+    Configs change speed only, never results."""
+    global _TABLE
+    if path is None:
+        _TABLE = None
+        return
+    raw = json.loads(Path(path).read_text())
+    _TABLE = {tuple(int(v) for v in nk.split(",")): {int(m): tuple(c) for m, c in row.items()}
+              for nk, row in raw.items()}
+
+
+# Built-in gfx950 configs when a shape has no table entry (speed only).
+DEFAULT_CFGS = ((16, (16, 64, 128, 8, 1, 8, 1)), (32, (32, 64, 128, 8, 1, 8, 1)), (64, (64, 64, 128, 4, 1, 8, 1)))
+LARGE_M_CFG = (64, 64, 128, 4, 1, 8, 1)
+
+
+def _cfg(M, N, Kd):
+    """Config for an (M, N, K) call: the table row of the smallest tuned M >= M; beyond the
+    largest tuned M the largest row with SK = 1; otherwise a built-in (plugin.py:37-48)."""
+    if _TABLE is not None and (N, Kd) in _TABLE:
+        row = _TABLE[(N, Kd)]
+        ms = sorted(row)
+        if M > ms[-1]:
+            return tuple(row[ms[-1]][:6]) + (1,)
+        return row[next(m for m in ms if m >= M)]
+    for bound, cfg in DEFAULT_CFGS:
+        if M <= bound:
+            return cfg
+    return LARGE_M_CFG
+
+
+@torch.library.custom_op("exactmm::linear", mutates_args=())
+def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: torch.Tensor,
+                    sw: torch.Tensor) -> torch.Tensor:
+    """y = x @ W^T through the exact path: reshape to 2-D, digitize x (bf16 read directly),
+    exact matmul straight into an x.dtype output, in row blocks of RB (plugin.py:51-64)."""
+    shp = x.shape
+    N = wh.shape[0]
+    x2 = x.reshape(-1, shp[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M, Kd = x2.shape
+    out = x.new_empty(M, N)
+    for i in range(0, M, RB):
+        xb = x2[i:i + RB]
+        xd = K.digitize(xb, F)
+        K.exact_linear(xd, (wh, wl, cw, sw), F, TRUNC, out=out[i:i + RB], cfg=_cfg(xb.shape[0], N, Kd))
+    return out.reshape(*shp[:-1], N)
+
+
+@exact_linear_op.register_fake
+def _(x, wh, wl, cw, sw):
+    return x.new_empty(*x.shape[:-1], wh.shape[0])
+
+
+def digitize_weight_rows(w):
+    """Digitize a weight matrix on the GPU in row blocks (plugin.py:72-79)."""
+    parts = [K.digitize(w[i:i + WEIGHT_RB].float().contiguous(), F) for i in range(0, w.shape[0], WEIGHT_RB)]
+    return tuple(torch.cat([p[j] for p in parts]).contiguous() for j in range(4))
+
+
+def _digitize_layer(layer):
+    h, l, cs, sh = digitize_weight_rows(layer.weight.data)
+    layer.register_buffer("ex_wh", h, persistent=False)
+    layer.register_buffer("ex_wl", l, persistent=False)
+    layer.register_buffer("ex_cw", cs, persistent=False)
+    layer.register_buffer("ex_sw", sh, persistent=False)
+
+
+def _apply(layer, x, bias):
+    y = torch.ops.exactmm.linear(x, layer.ex_wh, layer.ex_wl, layer.ex_cw, layer.ex_sw)
+    return y if bias is None else y + bias
+
+
+if HAVE_VLLM:
+
+    class ExactLinearMethod(UnquantizedLinearMethod):
+        def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+            _digitize_layer(layer)
+
+        def apply(self, layer, x, bias=None):
+            return _apply(layer, x, bias)
+
+    class ExactLMHeadMethod(UnquantizedEmbeddingMethod):
+        """lm_head through the exact linear layer; the embedding lookup is unchanged."""
+
+        def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+            _digitize_layer(layer)
+
+        def apply(self, layer, x, bias=None):
+            return _apply(layer, x, bias)
+
+    @register_quantization_config("exact_int8")
+    class ExactInt8Config(QuantizationConfig):
+        def __init__(self):
+            super().__init__()
+
+        def get_name(self):
+            return "exact_int8"
+
+        def get_supported_act_dtypes(self):
+            return [torch.bfloat16, torch.float16]
+
+        @classmethod
+        def get_min_capability(cls):
+            return 80
+
+        @staticmethod
+        def get_config_filenames():
+            return []
+
+        @classmethod
+        def from_config(cls, config):
+            return cls()
+
+        def get_quant_method(self, layer, prefix):
+            if isinstance(layer, LinearBase):
+                return ExactLinearMethod()
+            if LMHEAD and isinstance(layer, ParallelLMHead):
+                return ExactLMHeadMethod()
+            return None
