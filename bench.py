@@ -1,0 +1,285 @@
+"""Benchmark of the exact linear path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-attention] [--no-cpu]
+
+Step: one pass of the decode-shaped exact linear sweep (the BASELINE workload for this
+metric): QKV 4096->6144, O 4096->4096, gate_up 4096->24576 and down 12288->4096 at
+M in {1, 16, 64, 256}, F = 14 truncated (3 INT8 dots, the enable() default), each through
+the full exactmm::linear path (bf16 x -> digitize -> exact GEMM -> bf16 y). The step is a
+HIP graph; weights rotate over copies so no use finds its weights in the MALL/L2; inputs
+sit in HBM before timing starts. `value` is the sweep's algorithmic bytes
+(2NK + 2MK + 2MN + 8N per linear) over the step time.
+
+Also reported, from the same run:
+* per-op times with GB/s, TOPS and roofline fractions, and the hipBLASLt bf16 time;
+* `roofline` of the dominant kernel (the GEMM launch with the largest share of the step),
+  timed alone with HIP events on its own stream;
+* split-bf16 paged decode attention at H=32/KV=8/D=128/BS=16 for 64x8K, 16x16K, 256x1K (TB/s);
+* bit-exactness of the benchmarked outputs against the CPU oracle (sampled rows);
+* `cpu_baseline`: the C oracle (OpenMP) on a bounded sample of the same sweep, extrapolated
+  per op, on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "vllm-exact_amd"))
+
+METRIC = "exact GEMM INT8 TOPS (%MFMA peak) & GB/s (%HBM); decode-attn TB/s; bit-exact"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense INT8 MFMA, MI355X published
+SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288)]
+MS = [1, 16, 64, 256]
+F, TRUNC, NDOTS = 14, True, 3
+ATTN_CASES = [(64, 8192), (16, 16384), (256, 1024)]
+
+
+def gemm_bytes(M, N, K):
+    return 2 * N * K + 2 * M * K + 2 * M * N + 8 * N
+
+
+def gemm_ops(M, N, K, ndots=NDOTS):
+    return ndots * 2 * M * N * K
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
+                    help="exact_int8 tuning table to use")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the exact linear path is a per-GPU kernel "
+                                   "library (multi-GPU sharding is a design note); run with --gpus 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from vllm_exact import _native
+    from vllm_exact import kernels as K
+    from vllm_exact import paged_attn as P
+    from vllm_exact import plugin
+    from vllm_exact.graph_timing import rotations_for, time_graph
+
+    _native.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    plugin.load_table(args.table)
+    plugin.F, plugin.TRUNC = F, TRUNC
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    # ---------------------------------------------------------------- weights and inputs
+    total_w = sum(2 * N * Kd for _, N, Kd in SHAPES)
+    rot = rotations_for(total_w, min_total=3 * total_w, min_rot=3)
+    weights = {}
+    for name, N, Kd in SHAPES:
+        w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        weights[name] = [plugin.digitize_weight_rows(w) for _ in range(rot)]
+        weights[name + ".bf16"] = w
+    xs = {(M, Kd): torch.randn(M, Kd, device=dev, generator=gen).to(torch.bfloat16)
+          for M in MS for Kd in {k for _, _, k in SHAPES}}
+    log(f"weights: {total_w / 1e6:.0f} MB of digits per copy, {rot} copies")
+
+    ops = [(M, name, N, Kd) for M in MS for name, N, Kd in SHAPES]
+
+    def op_call(M, name, Kd, r, out=None):
+        wd = weights[name][r]
+        return torch.ops.exactmm.linear(xs[(M, Kd)], *wd)
+
+    # ---------------------------------------------------------------- the step graph
+    def step_calls(r):
+        # each op uses copy (r + op index) % rot, so consecutive uses of a shape's weights differ
+        for i, (M, name, N, Kd) in enumerate(ops):
+            op_call(M, name, Kd, (r + i) % rot)
+
+    for r in range(rot):
+        step_calls(r)
+    torch.cuda.synchronize()
+    graphs = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step_calls(0)
+    torch.cuda.current_stream().wait_stream(side)
+    for r in range(rot):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step_calls(r)
+        graphs.append(g)
+    for i in range(args.warmup):
+        graphs[i % rot].replay()
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    st.record()
+    for i in range(args.steps):
+        graphs[i % rot].replay()
+    en.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = st.elapsed_time(en) / args.steps
+    step_bytes = sum(gemm_bytes(M, N, Kd) for M, _, N, Kd in ops)
+    step_ops = sum(gemm_ops(M, N, Kd) for M, _, N, Kd in ops)
+    value = step_bytes / (step_ms * 1e-3) / 1e9
+    log(f"step {step_ms:.3f} ms (wall {wall * 1e3 / args.steps:.3f} ms), {value:.1f} GB/s")
+    del graphs
+
+    # ---------------------------------------------------------------- per-op detail
+    per_op = []
+    for M, name, N, Kd in ops:
+        cfg = plugin._cfg(M, N, Kd)
+        xd = K.digitize(xs[(M, Kd)], F)
+        t_op = time_graph(lambda r: op_call(M, name, Kd, r), rot)
+        t_gemm = time_graph(lambda r: K.exact_linear(xd, weights[name][r], F, TRUNC, cfg=cfg), rot)
+        wb = weights[name + ".bf16"]
+        wbs = [wb.clone() for _ in range(min(rot, rotations_for(2 * N * Kd)))]
+        t_bf16 = time_graph(lambda r: torch.matmul(xs[(M, Kd)], wbs[r].T), len(wbs))
+        del wbs
+        b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
+        t_roof = max(b / (HBM_PEAK_GBS * 1e9), o / (INT8_PEAK_TOPS * 1e12)) * 1e6
+        rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
+                   bf16_hipblaslt_us=round(t_bf16, 2), gemm_GBps=round(b / t_gemm / 1e3, 1),
+                   gemm_TOPS=round(o / t_gemm / 1e6, 1), hbm_frac=round(b / t_gemm / 1e3 / HBM_PEAK_GBS, 3),
+                   mfma_frac=round(o / t_gemm / 1e6 / INT8_PEAK_TOPS, 3), roofline_frac=round(t_roof / t_gemm, 3),
+                   bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma",
+                   vs_bf16=round(t_op / t_bf16, 2))
+        per_op.append(rec)
+        log(json.dumps(rec))
+
+    # dominant kernel: the GEMM with the largest share of the step, timed alone on its stream
+    dom = max(per_op, key=lambda r: r["gemm_us"])
+    M, N, Kd, name = dom["M"], dom["N"], dom["K"], dom["op"]
+    cfg = tuple(dom["cfg"])
+    xd = K.digitize(xs[(M, Kd)], F)
+    kstream = torch.cuda.Stream()
+    with torch.cuda.stream(kstream):
+        t_kernel = time_graph(lambda r: K.exact_linear(xd, weights[name][r], F, TRUNC, cfg=cfg), rot,
+                              calls_per_replay=20, replays=30)
+    b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
+    if dom["bound"] == "hbm":
+        roof = dict(bound="hbm", achieved=round(b / t_kernel / 1e3, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(b / t_kernel / 1e3 / HBM_PEAK_GBS, 4), traffic=None)
+    else:
+        roof = dict(bound="mfma", achieved=round(o / t_kernel / 1e6, 1), peak=INT8_PEAK_TOPS, unit="TFLOP/s",
+                    frac=round(o / t_kernel / 1e6 / INT8_PEAK_TOPS, 4), traffic=None)
+    roof.update(kernel=f"exact GEMM M={M} {name} {N}x{Kd} cfg={list(cfg)}", kernel_us=round(t_kernel, 2),
+                algorithmic_bytes=b, algorithmic_ops=o)
+    log("roofline:", json.dumps(roof))
+
+    # ---------------------------------------------------------------- bit-exactness of the outputs
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle  # the checker only
+
+    exact_ok = True
+    for M, name, N, Kd in [(16, "o", 4096, 4096), (256, "down", 4096, 12288), (1, "qkv", 6144, 4096)]:
+        y = op_call(M, name, Kd, 0).float().cpu().numpy()
+        wd = tuple(t.cpu().numpy() for t in weights[name][0])
+        rows = np.arange(min(M, 8))
+        xdn = oracle.digitize_c(xs[(M, Kd)].float().cpu().numpy()[rows], F)
+        ref = oracle.exact_linear_c(xdn, wd, F, TRUNC)
+        want = oracle.bf16_rne_c(ref).reshape(ref.shape)
+        got = torch.from_numpy(y[rows]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        exact_ok &= bool(np.array_equal(got, want))
+    log("bit-exact vs oracle:", exact_ok)
+
+    # ---------------------------------------------------------------- attention
+    attn = []
+    if not args.no_attention:
+        H, KV, D, BS = 32, 8, 128, 16
+        P.MAX_LEN = 16384
+        for B, L in ATTN_CASES:
+            nbp = L // BS
+            nblocks = B * nbp
+            kv = torch.randn(nblocks, KV, BS, 2 * D, device=dev, generator=gen, dtype=torch.bfloat16)
+            bt = torch.randperm(nblocks, device=dev, generator=gen).view(B, nbp).to(torch.int32)
+            q = torch.randn(B, H, D, device=dev, generator=gen, dtype=torch.bfloat16)
+            sl = torch.full((B,), L, device=dev, dtype=torch.int32)
+            kc, vc = kv.transpose(1, 2).split(D, dim=-1)
+            out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+            t = time_graph(lambda r: P.paged_decode(q, kc, vc, bt, sl, D ** -0.5, out, B, L), 1,
+                           calls_per_replay=10, replays=20)
+            kv_bytes = B * L * KV * D * 2 * 2
+            rec = dict(B=B, L=L, us=round(t, 2), kv_bytes=kv_bytes, TBps=round(kv_bytes / t / 1e6, 3),
+                       hbm_frac=round(kv_bytes / t / 1e3 / HBM_PEAK_GBS, 3))
+            attn.append(rec)
+            log(json.dumps(rec))
+            del kv, kc, vc
+            torch.cuda.empty_cache()
+
+    # ---------------------------------------------------------------- CPU baseline (oracle, sampled)
+    cpu = None
+    if not args.no_cpu:
+        threads = oracle.cpu_threads()
+        rng = np.random.default_rng(0)
+        samples = {}
+        for name, N, Kd in SHAPES:
+            ns = min(N, 2048)
+            w = (rng.standard_normal((ns, Kd)) * 0.02).astype(np.float32)
+            samples[name] = (ns, oracle.digitize_c(w, F))
+        total_s, sample_desc = 0.0, []
+        min_s = args.cpu_seconds / len(ops)
+        for M, name, N, Kd in ops:
+            ns, wd = samples[name]
+            x = rng.standard_normal((M, Kd)).astype(np.float32)
+            reps, t0 = 0, time.perf_counter()
+            while True:
+                xdn = oracle.digitize_c(x, F)
+                oracle.exact_linear_c(xdn, wd, F, TRUNC)
+                reps += 1
+                dt = (time.perf_counter() - t0) / reps
+                if reps * dt >= min_s / 4 or reps >= 50:
+                    break
+            total_s += dt * N / ns
+            sample_desc.append(f"M={M} {name} {ns}/{N} rows x{reps}")
+        cpu = dict(value=round(step_bytes / total_s / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                   sample="C oracle (digitize + exact integer digit dots, OpenMP) on the first rows of every op "
+                          "of the sweep, time extrapolated linearly in N: " + "; ".join(sample_desc),
+                   step_ms_extrapolated=round(total_s * 1e3, 1))
+        log("cpu baseline:", json.dumps(cpu))
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "decode-shaped exact linear sweep: QKV 4096->6144, O 4096->4096, gate_up "
+                               "4096->24576, down 12288->4096 at M in {1,16,64,256}; bf16 in/out, F=14 truncated "
+                               "(3 INT8 dots), full exactmm::linear op (digitize + GEMM), weights rotated past MALL",
+                   "F": F, "trunc": TRUNC, "step_algorithmic_bytes": step_bytes, "step_int8_ops": step_ops,
+                   "step_TOPS": round(step_ops / (step_ms * 1e-3) / 1e12, 2)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "bit_exact": exact_ok,
+        "per_op": per_op,
+        "attention": attn,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

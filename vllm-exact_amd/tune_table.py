@@ -1,0 +1,98 @@
+"""Build a gfx950 tuning table for the exact plugin (the reference's scripts/tune_table.py).
+
+    python vllm-exact_amd/tune_table.py OUT.json [--f 14] [--shapes 6144x4096,4096x4096,...]
+                                                 [--ms 1,16,64,256] [--report OUT_report.json]
+
+For each weight shape (N, K) and batch bucket M, every candidate config is run, checked
+bitwise against the first candidate's output (exact integer accumulation makes every
+tiling give the same bits; a mismatch raises), and timed by HIP-graph replay with the
+weights rotated over enough copies to stream past the 256 MB MALL. The fastest config is
+written to {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK]}}; the report also records the
+bf16 hipBLASLt time of the same product (torch.matmul) for comparison.
+"""
+import argparse
+import itertools
+import json
+import sys
+from pathlib import Path
+
+import torch
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+from vllm_exact import kernels as K  # noqa: E402
+from vllm_exact.graph_timing import rotations_for, time_graph  # noqa: E402
+
+DEFAULT_SHAPES = "6144x4096,4096x4096,24576x4096,4096x12288,151936x4096,10240x4096,12288x4096"
+BASE_CFGS = [(bm, bn, 128, wv, 1, 8) for bm, bn, wv in itertools.product((16, 32, 64), (64, 128, 256), (4, 8))]
+SPLITS = (1, 2, 4, 8)
+
+
+def candidates(M, Kd):
+    out = []
+    for c in BASE_CFGS:
+        if c[0] > max(16, 1 << max(0, (M - 1).bit_length())):
+            continue
+        for sk in SPLITS:
+            if sk > 1 and Kd // sk < 256:
+                continue
+            out.append(c + (sk,))
+    return out
+
+
+def tune_shape(N, Kd, ms, F, trunc, gen, report):
+    w = (torch.randn(N, Kd, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+    rot = rotations_for(2 * N * Kd)
+    wds = [K.digitize(w, F) for _ in range(rot)]
+    row = {}
+    for M in ms:
+        x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
+        xd = K.digitize(x, F)
+        ref, best, tried = None, None, []
+        for cfg in candidates(M, Kd):
+            try:
+                y = K.exact_linear(xd, wds[0], F, trunc, cfg=cfg)
+            except NotImplementedError:
+                continue
+            if ref is None:
+                ref = y
+            elif not torch.equal(y.view(torch.int32), ref.view(torch.int32)):
+                raise RuntimeError(f"config {cfg} changed the result (N={N} K={Kd} M={M})")
+            t = time_graph(lambda i, c=cfg: K.exact_linear(xd, wds[i], F, trunc, cfg=c), rot)
+            tried.append((t, cfg))
+            if best is None or t < best[0]:
+                best = (t, cfg)
+        wbs = [w.clone() for _ in range(rot)]
+        t_bf16 = time_graph(lambda i: torch.matmul(x, wbs[i].T), rot)
+        del wbs
+        row[str(M)] = list(best[1])
+        rec = dict(N=N, K=Kd, M=M, exact_us=round(best[0], 2), bf16_hipblaslt_us=round(t_bf16, 2),
+                   cfg=list(best[1]), candidates=len(tried))
+        report.append(rec)
+        print(json.dumps(rec), flush=True)
+    del wds
+    torch.cuda.empty_cache()
+    return row
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("out")
+    ap.add_argument("--f", type=int, default=14)
+    ap.add_argument("--shapes", default=DEFAULT_SHAPES)
+    ap.add_argument("--ms", default="1,2,4,8,16,24,32,48,64,96,128,192,256")
+    ap.add_argument("--report", default=None)
+    args = ap.parse_args()
+    F, trunc = args.f, args.f == 14
+    shapes = [tuple(map(int, s.split("x"))) for s in args.shapes.split(",")]
+    ms = [int(m) for m in args.ms.split(",")]
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    table, report = {}, []
+    for N, Kd in shapes:
+        table[f"{N},{Kd}"] = tune_shape(N, Kd, ms, F, trunc, gen, report)
+    Path(args.out).write_text(json.dumps(table, indent=1))
+    rep = args.report or args.out.replace(".json", "_report.json")
+    Path(rep).write_text(json.dumps(report, indent=1))
+
+
+if __name__ == "__main__":
+    main()
