@@ -91,7 +91,7 @@ def main():
     weights = {}
     for name, N, Kd in SHAPES:
         w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
-        weights[name] = [plugin.digitize_weight_rows(w) for _ in range(rot)]
+        weights[name] = [plugin.pack_weight(w) for _ in range(rot)]
         weights[name + ".bf16"] = w
     xs = {(M, Kd): torch.randn(M, Kd, device=dev, generator=gen).to(torch.bfloat16)
           for M in MS for Kd in {k for _, _, k in SHAPES}}
@@ -99,9 +99,12 @@ def main():
 
     ops = [(M, name, N, Kd) for M in MS for name, N, Kd in SHAPES]
 
-    def op_call(M, name, Kd, r, out=None):
-        wd = weights[name][r]
-        return torch.ops.exactmm.linear(xs[(M, Kd)], *wd)
+    def op_call(M, name, Kd, r):
+        return torch.ops.exactmm.linear(xs[(M, Kd)], *weights[name][r])
+
+    def gemm_call(xd, name, Kd, r, cfg):
+        wp, _, cw, sw = weights[name][r]
+        return K.exact_linear_packed(xd, (wp, cw, sw), Kd, F, TRUNC, cfg=cfg)
 
     # ---------------------------------------------------------------- the step graph
     def step_calls(r):
@@ -145,9 +148,9 @@ def main():
     per_op = []
     for M, name, N, Kd in ops:
         cfg = plugin._cfg(M, N, Kd)
-        xd = K.digitize(xs[(M, Kd)], F)
+        xd = K.digitize_packed(xs[(M, Kd)], F)
         t_op = time_graph(lambda r: op_call(M, name, Kd, r), rot)
-        t_gemm = time_graph(lambda r: K.exact_linear(xd, weights[name][r], F, TRUNC, cfg=cfg), rot)
+        t_gemm = time_graph(lambda r: gemm_call(xd, name, Kd, r, cfg), rot)
         wb = weights[name + ".bf16"]
         wbs = [wb.clone() for _ in range(min(rot, rotations_for(2 * N * Kd)))]
         t_bf16 = time_graph(lambda r: torch.matmul(xs[(M, Kd)], wbs[r].T), len(wbs))
@@ -167,11 +170,10 @@ def main():
     dom = max(per_op, key=lambda r: r["gemm_us"])
     M, N, Kd, name = dom["M"], dom["N"], dom["K"], dom["op"]
     cfg = tuple(dom["cfg"])
-    xd = K.digitize(xs[(M, Kd)], F)
+    xd = K.digitize_packed(xs[(M, Kd)], F)
     kstream = torch.cuda.Stream()
     with torch.cuda.stream(kstream):
-        t_kernel = time_graph(lambda r: K.exact_linear(xd, weights[name][r], F, TRUNC, cfg=cfg), rot,
-                              calls_per_replay=20, replays=30)
+        t_kernel = time_graph(lambda r: gemm_call(xd, name, Kd, r, cfg), rot, calls_per_replay=20, replays=30)
     b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
     if dom["bound"] == "hbm":
         roof = dict(bound="hbm", achieved=round(b / t_kernel / 1e3, 1), peak=HBM_PEAK_GBS, unit="GB/s",
@@ -190,7 +192,7 @@ def main():
     exact_ok = True
     for M, name, N, Kd in [(16, "o", 4096, 4096), (256, "down", 4096, 12288), (1, "qkv", 6144, 4096)]:
         y = op_call(M, name, Kd, 0).float().cpu().numpy()
-        wd = tuple(t.cpu().numpy() for t in weights[name][0])
+        wd = oracle.digitize_c(weights[name + ".bf16"].float().cpu().numpy(), F)
         rows = np.arange(min(M, 8))
         xdn = oracle.digitize_c(xs[(M, Kd)].float().cpu().numpy()[rows], F)
         ref = oracle.exact_linear_c(xdn, wd, F, TRUNC)

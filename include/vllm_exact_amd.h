@@ -93,6 +93,35 @@ int vxa_exact_linear(const int8_t* xh, const int8_t* xl, const int32_t* cx, cons
                      void* ws, size_t ws_bytes, vxa_stream_t stream);
 
 /*
+ * Fragment-major packed digits (the operand order of v_mfma_i32_16x16x64_i8).
+ * A [rows, k] pair of digit planes (h, l) packs into cdiv(rows,16) x cdiv(k,64) blocks of
+ * 2 KiB: block (rt, kt) = [h fragment | l fragment], fragment byte 16*lane + j holding
+ * row 16*rt + (lane & 15), column 64*kt + 16*(lane >> 4) + j; rows >= rows and columns >= k
+ * are zero digits. Each MFMA operand is then 1 KiB of contiguous memory. Weights are packed
+ * once at load time (the reference digitizes them there, plugin.py:72-79); activations are
+ * digitized straight into the packed form. No reference counterpart: the reference keeps
+ * row-major digits only. vxa_packed_bytes returns the packed size.
+ */
+size_t vxa_packed_bytes(int64_t rows, int64_t k);
+int vxa_pack_digits(const int8_t* h, const int8_t* l, int64_t rows, int64_t k, int64_t ldd,
+                    int8_t* packed, vxa_stream_t stream);
+/* digitize (same bits as vxa_digitize) writing the packed layout; cs, sh as vxa_digitize. */
+int vxa_digitize_packed(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                        int8_t* packed, int32_t* cs, int32_t* sh, int f, vxa_stream_t stream);
+/*
+ * vxa_exact_linear on packed operands: same arithmetic, same bits, same cfg and split-K
+ * semantics (the plan uses k rounded up to a multiple of 64). xp / wp are packed digits of
+ * x [m, k] and w [n, k]. This is the entry point the exactmm::linear op uses for weights
+ * packed at load time (plugin.py:51-64 replaces the row-major call there).
+ */
+int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, const int32_t* sx,
+                            const int8_t* wp, const int32_t* cw, const int32_t* sw,
+                            void* out, int out_dtype, int64_t ldo,
+                            int64_t m, int64_t n, int64_t k, int f, int trunc,
+                            const int32_t* cfg, int cfg_len,
+                            void* ws, size_t ws_bytes, vxa_stream_t stream);
+
+/*
  * Workspace bytes for vxa_paged_decode: fp32 segment partials m, l [n, H, NS] and
  * acc [n, H, NS, D] with NS = max(1, cdiv(max_len, split)) (paged_attn.py:105-108).
  * Zero when NS == 1 (every request then finishes inside one segment).

@@ -61,3 +61,22 @@ def make_paged(B, L, BS, H, KV, D, seed=0, spare=7, var_len=True, kv_scale=1.0):
 def kv_views(kv, D):
     """key/value views (num_blocks, BS, KV, D) of a [num_blocks, KV, BS, 2D] cache."""
     return kv.transpose(1, 2).split(D, dim=-1)
+
+
+def pack_np(h, l):
+    """Fragment-major layout written out in numpy, as documented for vxa_pack_digits:
+    block (rt, kt) = [h fragment | l fragment], fragment byte 16*lane + j = row 16rt + (lane & 15),
+    column 64kt + 16(lane >> 4) + j; padding rows/columns are zero."""
+    R, K = h.shape
+    RT, KT = (R + 15) // 16, (K + 63) // 64
+    out = np.zeros((RT, KT, 2, 64, 16), np.int8)
+    hp = np.zeros((RT * 16, KT * 64), np.int8)
+    lp = np.zeros((RT * 16, KT * 64), np.int8)
+    hp[:R, :K] = h
+    lp[:R, :K] = l
+    lane = np.arange(64)
+    for plane, src in ((0, hp), (1, lp)):
+        blk = src.reshape(RT, 16, KT, 4, 16)  # rt, r16, kt, kq, j
+        # lane = 16*kq + r16
+        out[:, :, plane] = blk.transpose(0, 2, 3, 1, 4).reshape(RT, KT, 64, 16)[:, :, lane]
+    return out.reshape(RT, KT, 2, 1024)

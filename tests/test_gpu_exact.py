@@ -23,7 +23,9 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 REF_CFGS = ((16, 64, 128, 4, 3, 8), (64, 128, 128, 4, 4, 8), (16, 128, 256, 8, 3, 8))  # tests/test_gpu.py:27
-OWN_CFGS = ((16, 64, 128, 8, 1, 8), (16, 256, 128, 4, 1, 8), (32, 128, 128, 8, 1, 8), (64, 64, 128, 4, 1, 8))
+OWN_CFGS = ((16, 64, 128, 8, 1, 8), (16, 256, 128, 4, 1, 8), (32, 128, 128, 8, 1, 8), (64, 64, 128, 4, 1, 8),
+            (16, 16, 128, 16, 4, 8), (32, 32, 128, 8, 2, 8), (64, 32, 128, 8, 1, 8), (128, 128, 128, 4, 4, 8),
+            (64, 64, 128, 4, 8, 8), (128, 64, 128, 4, 6, 8))
 
 
 def _bf16_of(ref_f32):
@@ -49,7 +51,7 @@ def test_digitize_bf16_input(F):
 
 @pytest.mark.parametrize("F", [14, 15])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("R,Kd", [(16, 4096), (7, 1000), (1, 12288), (33, 24), (5, 1001)])
+@pytest.mark.parametrize("R,Kd", [(16, 4096), (7, 1000), (1, 12288), (33, 24), (5, 1001), (3, 40000), (2, 40001)])
 def test_digitize_matches_oracle(F, dtype, R, Kd):
     x, _ = xw(R, 1, Kd, seed=R + Kd)
     x[0] = 0.0  # zero row
@@ -137,8 +139,9 @@ def test_config1_single_linear_bitwise():
 
 
 DECODE_SHAPES = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096), "down": (4096, 12288)}
-SWEEP_CFGS = ((16, 64, 128, 4, 1, 8), (16, 64, 128, 8, 1, 8), (16, 128, 128, 4, 1, 8), (16, 256, 128, 8, 1, 8),
-              (32, 128, 128, 8, 1, 8), (64, 64, 128, 4, 1, 8))
+SWEEP_CFGS = ((16, 64, 128, 4, 1, 8), (16, 16, 128, 16, 4, 8), (16, 32, 128, 8, 2, 8), (16, 256, 128, 8, 1, 8),
+              (32, 128, 128, 8, 1, 8), (64, 64, 128, 4, 1, 8), (64, 64, 128, 4, 4, 8), (128, 128, 128, 4, 4, 8),
+              (64, 128, 128, 4, 6, 8))
 
 
 @pytest.mark.parametrize("shape", list(DECODE_SHAPES))
@@ -190,7 +193,8 @@ def test_lm_head_wide_n_bitwise(M):
     xd_np = np_digits(xd)
     for tr in (True, False):
         y = K.exact_linear(xd, wd, F, tr, cfg=(16, 64, 128, 8, 1, 8, 1))
-        for cfg in ((16, 256, 128, 8, 1, 8, 2), (64, 64, 128, 4, 1, 8, 4)):
+        for cfg in ((16, 256, 128, 8, 1, 8, 2), (64, 64, 128, 4, 1, 8, 4), (128, 128, 128, 4, 4, 8, 1),
+                    (16, 32, 128, 16, 2, 8, 1)):
             assert torch.equal(K.exact_linear(xd, wd, F, tr, cfg=cfg).view(torch.int32), y.view(torch.int32))
         rows = np.arange(M) if M <= 16 else np.array([0, 1, 128, 255])
         ref = oracle.exact_linear_c(tuple(t[rows] for t in xd_np), wd_np, F, tr)

@@ -1,0 +1,78 @@
+"""GPU parity of the packed (fragment-major) path.
+
+The packed layout has no counterpart in the reference; tests/helpers.pack_np states it
+independently in numpy. Checks: GPU packing matches it byte for byte; digitize_packed equals
+pack(digitize) and the oracle's digits; the packed GEMM equals the oracle bitwise for both
+kernel families, ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
+exactmm::linear op on load-time packed weights equals the oracle.
+"""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import f32_bits, np_digits, pack_np, stress_xw, xw
+from vllm_exact import kernels as K
+from vllm_exact import plugin
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+PACKED_CFGS = ((16, 16, 128, 16, 4, 8), (16, 32, 128, 8, 2, 8), (16, 64, 128, 4, 1, 8), (32, 64, 128, 8, 1, 8),
+               (64, 32, 128, 4, 2, 8), (64, 64, 128, 4, 1, 8), (64, 64, 128, 4, 8, 8), (128, 64, 128, 4, 6, 8),
+               (64, 128, 128, 4, 4, 8), (128, 128, 128, 4, 4, 8), (128, 128, 128, 4, 2, 8))
+
+
+@pytest.mark.parametrize("R,Kd", [(16, 4096), (37, 1000), (5, 64), (300, 12288), (3, 40000)])
+def test_pack_matches_layout_and_digitize_packed(R, Kd):
+    x, _ = xw(R, 1, Kd, seed=R)
+    for F in (14, 15):
+        d = K.digitize(x.to(DEV), F)
+        packed, cs, sh = K.pack_digits(d)
+        dn = np_digits(d)
+        want = pack_np(dn[0], dn[1])
+        assert np.array_equal(packed.cpu().numpy(), want)
+        pd, pcs, psh = K.digitize_packed(x.to(DEV).to(torch.bfloat16).float(), F)
+        xbd = oracle.digitize_c(x.to(torch.bfloat16).float().numpy(), F)
+        assert np.array_equal(pd.cpu().numpy(), pack_np(xbd[0], xbd[1]))
+        assert np.array_equal(pcs.cpu().numpy(), xbd[2]) and np.array_equal(psh.cpu().numpy(), xbd[3])
+        # bf16 input directly gives the same packed digits
+        pd2, _, _ = K.digitize_packed(x.to(DEV).to(torch.bfloat16), F)
+        assert torch.equal(pd2, pd)
+
+
+@pytest.mark.parametrize("F,tr", [(14, True), (14, False), (15, False)])
+@pytest.mark.parametrize("M,N,Kd", [(1, 64, 4096), (16, 4096, 4096), (24, 384, 4096), (5, 200, 12288),
+                                    (256, 1024, 4096), (300, 256, 12288), (33, 130, 1000)])
+def test_packed_gemm_bitwise(F, tr, M, N, Kd):
+    x, w = stress_xw(M, N, Kd, seed=M + N)
+    xd, wd = K.digitize(x.to(DEV), F), K.digitize(w.to(DEV), F)
+    ref = f32_bits(oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr))
+    xp, wp = K.pack_digits(xd), K.pack_digits(wd)
+    for base, sk in itertools.product(PACKED_CFGS, (1, 2, 4, 8)):
+        cfg = base + (sk,)
+        y = K.exact_linear_packed(xp, wp, Kd, F, tr, cfg=cfg)
+        assert np.array_equal(f32_bits(y.cpu().numpy()), ref), cfg
+    yb = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    K.exact_linear_packed(xp, wp, Kd, F, tr, out=yb, cfg=(16, 64, 128, 4, 1, 8, 2))
+    want_b = oracle.bf16_rne_c(oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr)).reshape(M, N)
+    assert np.array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), want_b)
+
+
+@pytest.mark.parametrize("shape", [(6144, 4096), (24576, 4096), (4096, 12288)])
+def test_op_with_packed_weights_matches_oracle(shape):
+    N, Kd = shape
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)
+    wbuf = plugin.pack_weight(w.to(DEV))
+    wd_np = oracle.digitize_c(w.float().numpy(), plugin.F)
+    for M in (1, 16, 64, 256):
+        x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+        y = torch.ops.exactmm.linear(x.to(DEV), *wbuf)
+        rows = np.arange(M) if M <= 64 else np.array([0, 100, 255])
+        xd_np = oracle.digitize_c(x.float().numpy()[rows], plugin.F)
+        ref = oracle.exact_linear_c(xd_np, wd_np, plugin.F, plugin.TRUNC)
+        got = y.cpu().view(torch.int16).numpy().view(np.uint16)[rows]
+        assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape)), M

@@ -50,6 +50,12 @@ __device__ inline float shfl_xor_f32(float v, int mask) {
   return shfl_f32(v, lane ^ mask);
 }
 
+// Single-pass digitize (digitize_fast.hip) into row-major planes (h, l, ldd) or, when
+// `packed`, the fragment-major layout at h. hipErrorInvalidValue: K needs the multi-pass path.
+hipError_t launch_digitize_fast(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int vec, int8_t* h,
+                                int8_t* l, int64_t ldd, bool packed, int32_t* cs, int32_t* sh, int F,
+                                hipStream_t st);
+
 #define VXA_CHECK_LAUNCH()                         \
   do {                                             \
     if (hipGetLastError() != hipSuccess) return VXA_ERR_LAUNCH; \

@@ -9,8 +9,10 @@
 // outside the scheme's domain (absmax < 2^(F-128), Inf or NaN), where the bits are
 // whatever the formula gives.
 //
-// One workgroup of 256 lanes per row; pass 1 reduces the row absmax, pass 2 re-reads the
-// row (now in L2) and writes both digit planes with vector stores.
+// This file holds the multi-pass kernel for rows longer than the single-pass kernel takes
+// (digitize_fast.hip, up to 32768 columns), and the C-ABI entry point. One workgroup of
+// 256 lanes per row; pass 1 reduces the row absmax, pass 2 re-reads the row (now in L2)
+// and writes both digit planes with vector stores.
 
 #include "common.h"
 
@@ -197,7 +199,13 @@ extern "C" int vxa_digitize(const void* x, int x_dtype, int64_t rows, int64_t k,
   if (rows > 0x7FFFFFFFLL) return VXA_ERR_UNSUPPORTED;
   if (!x || !h || !l || !cs || !sh || ldx < k || ldd < k) return VXA_ERR_ARG;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err;
+  if (x_dtype != VXA_F32 && x_dtype != VXA_BF16 && x_dtype != VXA_F16) return VXA_ERR_ARG;
+  const int esize = x_dtype == VXA_F32 ? 4 : 2;
+  const int vec = ((uintptr_t)x % 16 == 0) && ((ldx * esize) % 16 == 0) && ((uintptr_t)h % 16 == 0) &&
+                  ((uintptr_t)l % 16 == 0) && (ldd % 16 == 0);
+  hipError_t err = k > 0 ? launch_digitize_fast(x, x_dtype, rows, k, ldx, vec, h, l, ldd, false, cs, sh, f, st)
+                         : hipErrorInvalidValue;
+  if (err != hipErrorInvalidValue) return err == hipSuccess ? VXA_OK : VXA_ERR_LAUNCH;
   switch (x_dtype) {
     case VXA_F32: err = dispatch_vec<VXA_F32>(x, rows, k, ldx, h, l, ldd, cs, sh, f, st); break;
     case VXA_BF16: err = dispatch_vec<VXA_BF16>(x, rows, k, ldx, h, l, ldd, cs, sh, f, st); break;

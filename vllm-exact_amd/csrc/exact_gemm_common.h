@@ -1,0 +1,81 @@
+// Shared pieces of the exact two-digit INT8 GEMM (exact_gemm*.hip).
+//
+// out[m, n] = fp32(fp64(tot) * 2^-(sx[m] + sw[n])) with
+//   tot = 2^16 * sum(xh*wh) + 2^8 * sum(xh*wl + xl*wh) [+ sum(xl*wl)]  [+ F=15 offset terms]
+// (kernels.py:89-100 integer closed form; device kernels kernels.py:104-177).
+// Products are int8 x int8 MFMA (v_mfma_i32_16x16x64_i8) into int32; the digit sums combine
+// in int64. Integer addition is exact and associative: no tiling or K partition changes a bit.
+#pragma once
+
+#include "common.h"
+
+struct ExactParams {
+  const int8_t* xh;
+  const int8_t* xl;
+  const int32_t* cx;
+  const int32_t* sx;
+  int64_t ldx;
+  const int8_t* wh;
+  const int8_t* wl;
+  const int32_t* cw;
+  const int32_t* sw;
+  int64_t ldw;
+  void* out;
+  int64_t ldo;
+  int32_t out_dtype;
+  int32_t offset;  // 1 when F == 15 (offset digits)
+  int64_t M, N, K;
+  int64_t kch;  // K extent of one split (multiple of 64)
+  int32_t sk;   // number of splits (gridDim.y)
+  int64_t* ws;  // int64 [sk][M][N] partial sums when sk > 1
+  // Packed operands (fragment-major layout, pack.hip): xh / wh point at the packed
+  // buffers, xl / wl are unused; KT = cdiv(K, 64) K tiles, kpad = 64 * KT.
+  int64_t KT;
+  int64_t kpad;
+};
+
+// Kernel family and shape picked from a cfg tuple.
+enum ExactFamily { kFamilySmall = 0, kFamilyLds = 1, kFamilyScalar = 2 };
+
+struct ExactPlan {
+  int family;
+  // small-M register-streaming kernel: MT x NT MFMA tiles per wave, NWK waves along K,
+  // C 64-wide K steps whose loads are issued together
+  int mt, nt, nwk, chunk;
+  // LDS pipeline kernel: BM x BN workgroup tile, S ring stages
+  int bm, bn, stages;
+  int64_t kch;
+  int32_t sk;
+};
+
+// int64 -> fp64 (exact: |tot| < 2^53) -> * 2^e (a power of two built from its bits,
+// kernels.py:152-155) -> fp32 (round to nearest even).
+__device__ inline float exact_epilogue(int64_t tot, int32_t sxm, int32_t swn) {
+  const int64_t e = -(int64_t)(sxm + swn);
+  const double scale = __longlong_as_double((e + 1023) << 52);
+  return (float)((double)tot * scale);
+}
+
+// F == 15: 128*(cx + cw) + 128*128*K (kernels.py:96-97, 148-151)
+__device__ inline int64_t offset_terms(const ExactParams& p, int64_t m, int64_t n) {
+  return 128 * ((int64_t)p.cx[m] + (int64_t)p.cw[n]) + 128 * 128 * p.K;
+}
+
+// Final value of one output element (or its int64 partial for split-K).
+__device__ inline void exact_store(const ExactParams& p, int split, int64_t m, int64_t n, int64_t tot) {
+  if (p.sk > 1) {
+    p.ws[((int64_t)split * p.M + m) * p.N + n] = tot;
+  } else {
+    if (p.offset) tot += offset_terms(p, m, n);
+    store_f32_as(p.out, p.out_dtype, m * p.ldo + n, exact_epilogue(tot, p.sx[m], p.sw[n]));
+  }
+}
+
+__device__ inline v4i mfma_i8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+
+// Host-side launchers implemented per family (exact_gemm_sm.hip, exact_gemm_lds.hip).
+// Return hipErrorInvalidValue for a shape no instantiation covers.
+hipError_t launch_exact_small(const ExactPlan& pl, const ExactParams& ep, bool trunc, bool packed, hipStream_t st);
+hipError_t launch_exact_lds(const ExactPlan& pl, const ExactParams& ep, bool trunc, bool packed, hipStream_t st);
+// True when the small-M kernel has an instantiation for (MT, NT, C, NWK).
+bool exact_small_supported(int mt, int nt, int chunk, int nwk);

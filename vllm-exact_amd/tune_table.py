@@ -6,12 +6,13 @@
 For each weight shape (N, K) and batch bucket M, every candidate config is run, checked
 bitwise against the first candidate's output (exact integer accumulation makes every
 tiling give the same bits; a mismatch raises), and timed by HIP-graph replay with the
-weights rotated over enough copies to stream past the 256 MB MALL. The fastest config is
+weights rotated over enough copies to stream past the 256 MB MALL. By default the weights
+are packed at load time and x is digitized packed, as exactmm::linear runs them (--layout
+plain tunes the row-major kernels instead). The fastest config is
 written to {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK]}}; the report also records the
 bf16 hipBLASLt time of the same product (torch.matmul) for comparison.
 """
 import argparse
-import itertools
 import json
 import sys
 from pathlib import Path
@@ -23,41 +24,53 @@ from vllm_exact import kernels as K  # noqa: E402
 from vllm_exact.graph_timing import rotations_for, time_graph  # noqa: E402
 
 DEFAULT_SHAPES = "6144x4096,4096x4096,24576x4096,4096x12288,151936x4096,10240x4096,12288x4096"
-BASE_CFGS = [(bm, bn, 128, wv, 1, 8) for bm, bn, wv in itertools.product((16, 32, 64), (64, 128, 256), (4, 8))]
-SPLITS = (1, 2, 4, 8)
+SPLITS = (1, 2, 4)
 
 
 def candidates(M, Kd):
+    """Every instantiated kernel shape whose M block does not exceed max(16, next_pow2(M)),
+    times the split-K factors (kernels.py:298 filters the same way)."""
     out = []
-    for c in BASE_CFGS:
+    for c in K.EXACT_CFGS:
         if c[0] > max(16, 1 << max(0, (M - 1).bit_length())):
             continue
+        if M <= 16 and c[0] >= 64 and c[4] >= 2:
+            continue  # the LDS-ring kernel needs a real M tile
         for sk in SPLITS:
             if sk > 1 and Kd // sk < 256:
                 continue
-            out.append(c + (sk,))
+            out.append(tuple(c) + (sk,))
     return out
 
 
-def tune_shape(N, Kd, ms, F, trunc, gen, report):
+def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
     w = (torch.randn(N, Kd, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
     rot = rotations_for(2 * N * Kd)
-    wds = [K.digitize(w, F) for _ in range(rot)]
+    if packed:
+        wds = [K.pack_digits(K.digitize(w, F)) for _ in range(rot)]
+    else:
+        wds = [K.digitize(w, F) for _ in range(rot)]
     row = {}
     for M in ms:
         x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
-        xd = K.digitize(x, F)
+        xd = K.digitize_packed(x, F) if packed else K.digitize(x, F)
+
+        def run(i, cfg):
+            if packed:
+                return K.exact_linear_packed(xd, wds[i], Kd, F, trunc, cfg=cfg)
+            return K.exact_linear(xd, wds[i], F, trunc, cfg=cfg)
+
         ref, best, tried = None, None, []
         for cfg in candidates(M, Kd):
             try:
-                y = K.exact_linear(xd, wds[0], F, trunc, cfg=cfg)
+                y = run(0, cfg)
             except NotImplementedError:
                 continue
             if ref is None:
                 ref = y
             elif not torch.equal(y.view(torch.int32), ref.view(torch.int32)):
                 raise RuntimeError(f"config {cfg} changed the result (N={N} K={Kd} M={M})")
-            t = time_graph(lambda i, c=cfg: K.exact_linear(xd, wds[i], F, trunc, cfg=c), rot)
+            t = time_graph(lambda i, c=cfg: run(i, c), rot)
             tried.append((t, cfg))
             if best is None or t < best[0]:
                 best = (t, cfg)
@@ -67,8 +80,9 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report):
         row[str(M)] = list(best[1])
         rec = dict(N=N, K=Kd, M=M, exact_us=round(best[0], 2), bf16_hipblaslt_us=round(t_bf16, 2),
                    cfg=list(best[1]), candidates=len(tried))
-        report.append(rec)
         print(json.dumps(rec), flush=True)
+        rec["all"] = sorted([round(t, 2), list(c)] for t, c in tried)
+        report.append(rec)
     del wds
     torch.cuda.empty_cache()
     return row
@@ -81,6 +95,8 @@ def main():
     ap.add_argument("--shapes", default=DEFAULT_SHAPES)
     ap.add_argument("--ms", default="1,2,4,8,16,24,32,48,64,96,128,192,256")
     ap.add_argument("--report", default=None)
+    ap.add_argument("--layout", default="packed", choices=["packed", "plain"],
+                    help="packed: weights packed at load (the exactmm::linear path); plain: row-major digits")
     args = ap.parse_args()
     F, trunc = args.f, args.f == 14
     shapes = [tuple(map(int, s.split("x"))) for s in args.shapes.split(",")]
@@ -88,7 +104,7 @@ def main():
     gen = torch.Generator(device="cuda").manual_seed(0)
     table, report = {}, []
     for N, Kd in shapes:
-        table[f"{N},{Kd}"] = tune_shape(N, Kd, ms, F, trunc, gen, report)
+        table[f"{N},{Kd}"] = tune_shape(N, Kd, ms, F, trunc, gen, report, args.layout == "packed")
     Path(args.out).write_text(json.dumps(table, indent=1))
     rep = args.report or args.out.replace(".json", "_report.json")
     Path(rep).write_text(json.dumps(report, indent=1))

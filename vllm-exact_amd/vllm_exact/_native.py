@@ -31,6 +31,10 @@ EXPORTED = (
     "vxa_digitize",
     "vxa_exact_linear_plan",
     "vxa_exact_linear",
+    "vxa_packed_bytes",
+    "vxa_pack_digits",
+    "vxa_digitize_packed",
+    "vxa_exact_linear_packed",
     "vxa_paged_decode_workspace",
     "vxa_paged_decode",
 )
@@ -49,6 +53,14 @@ _SIGNATURES = {
         _int,
         [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _int, _i64, _i64, _i64, _i64, _int, _int,
          ctypes.POINTER(_i32), _int, _vp, _sz, _vp],
+    ),
+    "vxa_packed_bytes": (_sz, [_i64, _i64]),
+    "vxa_pack_digits": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "vxa_digitize_packed": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp]),
+    "vxa_exact_linear_packed": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int,
+         _vp, _sz, _vp],
     ),
     "vxa_paged_decode_workspace": (_int, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
     "vxa_paged_decode": (

@@ -107,14 +107,100 @@ def exact_linear_torch(xd, wd, F, trunc=False):
     return (tot.double() * two_e).float()
 
 
-# gfx950 candidates (BM, BN, BK, waves, stages, GM): BM picks 16/32/64-row blocks, BN the
-# workgroup's 64/128/256 output columns, waves the workgroup size (waves share N first,
-# then K). BK only rounds split-K chunks; stages and GM are accepted for the reference's
-# format and do not change the gfx950 schedule.
-EXACT_CFGS = [(16, 64, 128, 4, 1, 8), (16, 64, 128, 8, 1, 8), (16, 128, 128, 4, 1, 8), (16, 128, 128, 8, 1, 8),
-              (16, 256, 128, 4, 1, 8), (16, 256, 128, 8, 1, 8), (32, 64, 128, 4, 1, 8), (32, 64, 128, 8, 1, 8),
-              (32, 128, 128, 4, 1, 8), (32, 128, 128, 8, 1, 8), (64, 64, 128, 4, 1, 8)]
-AUTOTUNE_SPLITS = (1, 2, 4, 8)
+# ======================= packed (fragment-major) digits =======================
+# A [R, K] digit matrix packs into int8 [cdiv(R,16), cdiv(K,64), 2, 1024]: block (rt, kt) holds
+# the h then l fragment of rows 16rt..16rt+15 and columns 64kt..64kt+63 in the operand order of
+# the int8 MFMA (lane l's 16 bytes: row l & 15, columns 16*(l >> 4)..+16), zero-padded. Every
+# MFMA operand is then one contiguous 1 KiB load. The weights of the plugin are packed once at
+# load time; activations are digitized straight into this form.
+def packed_shape(R, K):
+    return ((R + 15) // 16, (K + 63) // 64, 2, 1024)
+
+
+def pack_digits(d):
+    """Row-major digits (h, l, cs, sh) -> (packed, cs, sh) on the GPU."""
+    h, l, cs, sh = d
+    _require_gpu(h, "pack_digits")
+    R, K = h.shape
+    if h.stride(1) != 1 or l.stride(1) != 1 or h.stride(0) != l.stride(0) or l.shape != h.shape:
+        raise ValueError("pack_digits: h/l must be row-major int8 planes of one shape")
+    packed = torch.empty(packed_shape(R, K), dtype=torch.int8, device=h.device)
+    with torch.cuda.device(h.device):
+        _nx.check(_nx.lib().vxa_pack_digits(h.data_ptr(), l.data_ptr(), R, K, h.stride(0), packed.data_ptr(),
+                                            _nx.stream_handle(h.device)), "pack_digits")
+    return packed, cs, sh
+
+
+def digitize_packed(x, F, out=None):
+    """digitize() writing packed digits: returns (packed, cs, sh), the same digits as
+    pack_digits(digitize(x, F))."""
+    _require_gpu(x, "digitize_packed")
+    if x.dim() != 2:
+        raise ValueError(f"digitize_packed expects a 2-D tensor, got shape {tuple(x.shape)}")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    R, K = x.shape
+    dev = x.device
+    if out is None:
+        out = (torch.empty(packed_shape(R, K), dtype=torch.int8, device=dev),
+               torch.empty(R, dtype=torch.int32, device=dev), torch.empty(R, dtype=torch.int32, device=dev))
+    packed, cs, sh = out
+    if packed.shape != packed_shape(R, K) or not packed.is_contiguous() or packed.dtype != torch.int8:
+        raise ValueError("digitize_packed: packed must be a contiguous int8 tensor of packed_shape(R, K)")
+    with torch.cuda.device(dev):
+        _nx.check(_nx.lib().vxa_digitize_packed(x.data_ptr(), _nx.dtype_enum(x.dtype), R, K, x.stride(0),
+                                                packed.data_ptr(), cs.data_ptr(), sh.data_ptr(), F,
+                                                _nx.stream_handle(dev)), "digitize_packed")
+    return out
+
+
+def exact_linear_packed(xp, wp, K, F, trunc=False, out=None, cfg=None):
+    """exact_linear on packed digits xp = (packed_x, cx, sx), wp = (packed_w, cw, sw) with
+    inner dimension K: the same bits as exact_linear on the row-major digits."""
+    px, cx, sx = xp
+    pw, cw, sw = wp
+    _require_gpu(px, "exact_linear_packed")
+    M, N = sx.numel(), sw.numel()
+    if px.shape != packed_shape(M, K) or pw.shape != packed_shape(N, K):
+        raise ValueError("exact_linear_packed: packed shapes do not match (M, K) and (N, K)")
+    if not (px.is_contiguous() and pw.is_contiguous()):
+        raise ValueError("exact_linear_packed: packed digits must be contiguous")
+    dev = px.device
+    if out is None:
+        out = torch.empty((M, N), device=dev, dtype=torch.float32)
+    if out.shape != (M, N) or out.stride(1) != 1 or out.device != dev:
+        raise ValueError("exact_linear_packed: out must be an (M, N) row-major tensor")
+    if cfg is None:
+        raise ValueError("exact_linear_packed: pass a cfg (plugin._cfg or a tuning-table entry)")
+    kpad = ((K + 63) // 64) * 64
+    _, _, ws_bytes = _nx.exact_plan(M, N, kpad, cfg)
+    ws = torch.empty(ws_bytes // 8, dtype=torch.int64, device=dev) if ws_bytes else None
+    arr, n = _nx.cfg_array(cfg)
+    with torch.cuda.device(dev):
+        _nx.check(_nx.lib().vxa_exact_linear_packed(
+            px.data_ptr(), cx.data_ptr(), sx.data_ptr(), pw.data_ptr(), cw.data_ptr(), sw.data_ptr(),
+            out.data_ptr(), _nx.dtype_enum(out.dtype), out.stride(0), M, N, K, int(F), int(bool(trunc)), arr, n,
+            _nx.ptr(ws), ws_bytes, _nx.stream_handle(dev)), "exact_linear_packed")
+    return out
+
+
+# gfx950 kernel shapes, as cfg tuples (BM, BN, BK, warps, stages, GM). Two families:
+# * small-M register-streaming kernel: BM = 16*MT rows, BN = 16*NT columns per workgroup,
+#   `warps` waves splitting K, `stages` = K steps whose loads are issued together;
+# * LDS-ring kernel (BM, BN >= 64, 4 waves, stages >= 2): BM x BN tile, `stages`-deep ring
+#   of direct-to-LDS loads.
+# BK only rounds split-K chunks; GM is accepted for the reference's format.
+SMALL_SHAPES = [(1, 1, 1, 4), (1, 1, 1, 8), (1, 1, 1, 16), (1, 1, 2, 4), (1, 1, 2, 8), (1, 1, 2, 16), (1, 1, 4, 4),
+                (1, 1, 4, 8), (1, 1, 4, 16), (1, 2, 1, 4), (1, 2, 1, 8), (1, 2, 1, 16), (1, 2, 2, 4), (1, 2, 2, 8),
+                (1, 2, 2, 16), (1, 2, 4, 4), (1, 2, 4, 8), (1, 4, 1, 4), (1, 4, 1, 8), (1, 4, 1, 16), (1, 4, 2, 4),
+                (1, 4, 2, 8), (2, 1, 1, 4), (2, 1, 1, 8), (2, 1, 1, 16), (2, 1, 2, 4), (2, 1, 2, 8), (2, 2, 1, 4),
+                (2, 2, 1, 8), (2, 2, 1, 16), (2, 2, 2, 4), (2, 2, 2, 8), (2, 4, 1, 4), (2, 4, 1, 8), (4, 1, 1, 4),
+                (4, 1, 1, 8), (4, 1, 2, 4), (4, 1, 2, 8), (4, 2, 1, 4), (4, 2, 1, 8), (4, 4, 1, 4)]  # (MT, NT, C, NWK)
+LDS_SHAPES = [(64, 64, 2), (64, 64, 4), (64, 64, 8), (128, 64, 2), (128, 64, 4), (128, 64, 6), (64, 128, 2),
+              (64, 128, 4), (64, 128, 6), (128, 128, 2), (128, 128, 3), (128, 128, 4)]  # (BM, BN, stages)
+EXACT_CFGS = ([(16 * mt, 16 * nt, 128, nwk, c, 8) for mt, nt, c, nwk in SMALL_SHAPES]
+              + [(bm, bn, 128, 4, st, 8) for bm, bn, st in LDS_SHAPES])
+AUTOTUNE_SPLITS = (1, 2, 4)
 _CFG_CACHE = {}
 
 
@@ -206,4 +292,5 @@ def autotune_exact(xd, wd, F, trunc):
 
 
 __all__ = ["HAVE_HIP", "HAVE_TRITON", "digitize_torch", "digitize_weight", "digitize", "exact_linear_torch",
-           "exact_linear", "autotune_exact", "EXACT_CFGS"]
+           "exact_linear", "autotune_exact", "EXACT_CFGS", "pack_digits", "digitize_packed", "exact_linear_packed",
+           "packed_shape"]

@@ -66,36 +66,61 @@ def _cfg(M, N, Kd):
 def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: torch.Tensor,
                     sw: torch.Tensor) -> torch.Tensor:
     """y = x @ W^T through the exact path: reshape to 2-D, digitize x (bf16 read directly),
-    exact matmul straight into an x.dtype output, in row blocks of RB (plugin.py:51-64)."""
+    exact matmul straight into an x.dtype output, in row blocks of RB (plugin.py:51-64).
+
+    Weights come either as the reference's row-major digit planes wh, wl [N, K], or packed
+    at load time (wh = packed [cdiv(N,16), cdiv(K,64), 2, 1024], wl empty); N is sw's length
+    either way, and both give the same bits."""
     shp = x.shape
-    N = wh.shape[0]
+    N = sw.shape[0]
     x2 = x.reshape(-1, shp[-1])
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     M, Kd = x2.shape
     out = x.new_empty(M, N)
+    packed = wh.dim() == 4
     for i in range(0, M, RB):
         xb = x2[i:i + RB]
-        xd = K.digitize(xb, F)
-        K.exact_linear(xd, (wh, wl, cw, sw), F, TRUNC, out=out[i:i + RB], cfg=_cfg(xb.shape[0], N, Kd))
+        cfg = _cfg(xb.shape[0], N, Kd)
+        if packed:
+            K.exact_linear_packed(K.digitize_packed(xb, F), (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
+        else:
+            K.exact_linear(K.digitize(xb, F), (wh, wl, cw, sw), F, TRUNC, out=out[i:i + RB], cfg=cfg)
     return out.reshape(*shp[:-1], N)
 
 
 @exact_linear_op.register_fake
 def _(x, wh, wl, cw, sw):
-    return x.new_empty(*x.shape[:-1], wh.shape[0])
+    return x.new_empty(*x.shape[:-1], sw.shape[0])
 
 
 def digitize_weight_rows(w):
-    """Digitize a weight matrix on the GPU in row blocks (plugin.py:72-79)."""
+    """Digitize a weight matrix on the GPU in row blocks (plugin.py:72-79): row-major digits."""
     parts = [K.digitize(w[i:i + WEIGHT_RB].float().contiguous(), F) for i in range(0, w.shape[0], WEIGHT_RB)]
     return tuple(torch.cat([p[j] for p in parts]).contiguous() for j in range(4))
 
 
+def pack_weight(w):
+    """Digitize and pack a weight matrix: (packed, empty, cw, sw), the buffers the op takes.
+    Row blocks of WEIGHT_RB keep the fp32 temporaries bounded (a multiple of 16 rows, so
+    blocks pack independently)."""
+    N, Kd = w.shape
+    packed = torch.empty(K.packed_shape(N, Kd), dtype=torch.int8, device=w.device)
+    cw = torch.empty(N, dtype=torch.int32, device=w.device)
+    sw = torch.empty(N, dtype=torch.int32, device=w.device)
+    for i in range(0, N, WEIGHT_RB):
+        rows = min(WEIGHT_RB, N - i)
+        src = w[i:i + rows]
+        if src.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            src = src.float()  # bf16/fp16/fp32 are read directly: same digits as their fp32 value
+        K.digitize_packed(src, F, out=(packed[i // 16:(i + rows + 15) // 16], cw[i:i + rows], sw[i:i + rows]))
+    return packed, torch.empty(0, dtype=torch.int8, device=w.device), cw, sw
+
+
 def _digitize_layer(layer):
-    h, l, cs, sh = digitize_weight_rows(layer.weight.data)
-    layer.register_buffer("ex_wh", h, persistent=False)
-    layer.register_buffer("ex_wl", l, persistent=False)
+    ph, pl, cs, sh = pack_weight(layer.weight.data)
+    layer.register_buffer("ex_wh", ph, persistent=False)
+    layer.register_buffer("ex_wl", pl, persistent=False)
     layer.register_buffer("ex_cw", cs, persistent=False)
     layer.register_buffer("ex_sw", sh, persistent=False)
 
