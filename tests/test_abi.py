@@ -54,6 +54,9 @@ def test_split_k_plan_follows_reference_arithmetic():
     # a single int32 accumulator never spans more than 32768 terms
     sk, kch, _ = _plan(1, 64, 65536, (16, 64, 128, 4, 3, 8, 1))
     assert kch <= 32768 and sk * kch >= 65536
+    # BK = 64 (x through LDS, weights in registers): chunks of whole 64-wide steps
+    assert _plan(256, 24576, 4096, (128, 192, 64, 4, 4, 8, 1)) == (1, 4096, 0)
+    assert _plan(33, 130, 1000, (64, 128, 64, 4, 3, 8, 3))[:2] == (3, 384)
     # mma (8th field) is accepted and does not change the plan
     assert _plan(24, 384, 4096, (64, 128, 128, 4, 4, 8, 2, 1)) == _plan(24, 384, 4096, (64, 128, 128, 4, 4, 8, 2, 0))
 

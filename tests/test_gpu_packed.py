@@ -2,8 +2,8 @@
 
 The packed layout has no counterpart in the reference; tests/helpers.pack_np states it
 independently in numpy. Checks: GPU packing matches it byte for byte; digitize_packed equals
-pack(digitize) and the oracle's digits; the packed GEMM equals the oracle bitwise for both
-kernel families, ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
+pack(digitize) and the oracle's digits; the packed GEMM equals the oracle bitwise for every
+kernel family (small-M, LDS ring, x through LDS with weights in registers), ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
 exactmm::linear op on load-time packed weights equals the oracle.
 """
 import itertools
@@ -22,7 +22,8 @@ DEV = "cuda"
 
 PACKED_CFGS = ((16, 16, 128, 16, 4, 8), (16, 32, 128, 8, 2, 8), (16, 64, 128, 4, 1, 8), (32, 64, 128, 8, 1, 8),
                (64, 32, 128, 4, 2, 8), (64, 64, 128, 4, 1, 8), (64, 64, 128, 4, 8, 8), (128, 64, 128, 4, 6, 8),
-               (64, 128, 128, 4, 4, 8), (128, 128, 128, 4, 4, 8), (128, 128, 128, 4, 2, 8))
+               (64, 128, 128, 4, 4, 8), (128, 128, 128, 4, 4, 8), (128, 128, 128, 4, 2, 8)) + tuple(
+    (bm, 4 * wn, 64, 4, r, 8) for bm, wn, r in K.XW_SHAPES)  # BK = 64: x through LDS, weights into registers
 
 
 @pytest.mark.parametrize("R,Kd", [(16, 4096), (37, 1000), (5, 64), (300, 12288), (3, 40000)])

@@ -35,14 +35,15 @@ struct ExactParams {
 };
 
 // Kernel family and shape picked from a cfg tuple.
-enum ExactFamily { kFamilySmall = 0, kFamilyLds = 1, kFamilyScalar = 2 };
+enum ExactFamily { kFamilySmall = 0, kFamilyLds = 1, kFamilyScalar = 2, kFamilyXw = 3 };
 
 struct ExactPlan {
   int family;
   // small-M register-streaming kernel: MT x NT MFMA tiles per wave, NWK waves along K,
   // C 64-wide K steps whose loads are issued together
   int mt, nt, nwk, chunk;
-  // LDS pipeline kernel: BM x BN workgroup tile, S ring stages
+  // LDS pipeline kernel: BM x BN workgroup tile, S ring stages; x-through-LDS kernel:
+  // BM x BN workgroup tile, `stages` = R weight register sets
   int bm, bn, stages;
   int64_t kch;
   int32_t sk;
@@ -71,6 +72,17 @@ __device__ inline void exact_store(const ExactParams& p, int split, int64_t m, i
   }
 }
 
+// Workgroups are handed to the 8 XCDs round-robin (linear id % 8), and each XCD has its own
+// L2. This bijection gives XCD x the logical ids [x*base + min(x, rem), ...) in dispatch
+// order, so neighbouring logical tiles (which share an operand tile) run on one XCD at about
+// the same time and meet in its L2.
+__device__ inline int64_t xcd_swizzle(int64_t lin, int64_t total) {
+  constexpr int64_t kXcd = 8;
+  const int64_t xcd = lin % kXcd, j = lin / kXcd;
+  const int64_t base = total / kXcd, rem = total % kXcd;
+  return xcd * base + (xcd < rem ? xcd : rem) + j;
+}
+
 __device__ inline v4i mfma_i8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 
 // Host-side launchers implemented per family (exact_gemm_sm.hip, exact_gemm_lds.hip).
@@ -79,3 +91,6 @@ hipError_t launch_exact_small(const ExactPlan& pl, const ExactParams& ep, bool t
 hipError_t launch_exact_lds(const ExactPlan& pl, const ExactParams& ep, bool trunc, bool packed, hipStream_t st);
 // True when the small-M kernel has an instantiation for (MT, NT, C, NWK).
 bool exact_small_supported(int mt, int nt, int chunk, int nwk);
+// Packed operands only (exact_gemm_xw.hip).
+hipError_t launch_exact_xw(const ExactPlan& pl, const ExactParams& ep, bool trunc, hipStream_t st);
+bool exact_xw_supported(int bm, int bn, int r, bool trunc);

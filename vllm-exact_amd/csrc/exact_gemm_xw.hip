@@ -1,0 +1,217 @@
+// Large-M exact GEMM on packed digits: the x tile through an LDS ring, the weight fragments
+// straight into registers.
+//
+// Workgroup tile BM x (4 * WN): 4 waves side by side along N, each computing all BM rows of
+// its WN columns. The x fragments of a K step (BM/16 tiles x 2 digit planes, 1 KiB each in
+// MFMA lane order) are shared by the 4 waves, so they go through a ring of S = R + 1 LDS
+// stages filled by global_load_lds_dwordx4 (gfx950 direct-to-LDS loads, a quarter of the
+// fragments per wave). The weight fragments of a wave are its own: each is one contiguous
+// 1 KiB global_load_dwordx4 per wave straight into a ring of R register sets, so the weight
+// stream (the HBM-bound operand) keeps R steps in flight per wave without using LDS.
+//
+// K step j:  s_waitcnt for the loads of step j (x stage and weight set) and for this wave's
+// LDS reads -> s_barrier (every wave's quarter of stage j landed, and every wave has finished
+// reading stage j-1) -> issue
+// the x loads of step j+R into the stage of step j-1 -> read stage j into registers ->
+// MFMAs -> issue the weight loads of step j+R into the register set of step j.
+// Every step issues the same loads (past the last step they repeat step nk-1 into a stage or
+// set no live step reads), so the wait count is one constant and the loop has no branch.
+//
+// Products and sums are the same int32 MFMA dot products as the other kernels; only the
+// order of integer additions differs, which changes no bit.
+
+#include "exact_gemm_common.h"
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int BM, int WN, int R, bool TRUNC>
+__global__ __launch_bounds__(256) void exact_xw_kernel(ExactParams p) {
+  constexpr int TM = BM / 16;     // 16-row tiles of x
+  constexpr int TN = WN / 16;     // 16-column tiles of one wave
+  constexpr int BN = 4 * WN;      // workgroup tile width
+  constexpr int S = R + 1;        // x ring stages
+  constexpr int NFX = 2 * TM;     // x fragments per stage (h and l planes)
+  constexpr int LX = NFX / 4;     // x fragments each wave loads per stage
+  constexpr int LW = 2 * TN;      // weight fragments each wave loads per step
+  constexpr int kWait = (R - 1) * (LX + LW);
+  static_assert(NFX % 4 == 0, "x fragments split evenly over the 4 waves");
+  static_assert(kWait <= 63, "vmcnt limit");
+  __shared__ __attribute__((aligned(1024))) int8_t ring[S * NFX * 1024];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  // Logical tile order: M tiles fastest, then N tiles, then K splits; the workgroups that
+  // share one weight tile are neighbours and, through xcd_swizzle, on one XCD.
+  const int64_t nbm = cdiv<int64_t>(p.M, BM);
+  const int64_t nbn = cdiv<int64_t>(p.N, BN);
+  const int64_t t = xcd_swizzle((int64_t)blockIdx.y * gridDim.x + blockIdx.x, (int64_t)gridDim.x * gridDim.y);
+  const int64_t bm = t % nbm;
+  const int64_t bn = (t / nbm) % nbn;
+  const int split = (int)(t / (nbm * nbn));
+  const int64_t m0 = bm * BM;
+  const int64_t n0 = bn * BN + wave * WN;
+  const int64_t kb = (int64_t)split * p.kch;
+  const int64_t ke = min(kb + p.kch, p.kpad);
+  const int64_t nk = (ke - kb) >> 6;
+  const int64_t kt0 = kb >> 6;
+
+  // x fragments this wave copies into each stage (tiles past M clamped: rows >= M are never stored)
+  const int8_t* xsrc[LX];
+  int xdst[LX];
+#pragma unroll
+  for (int i = 0; i < LX; ++i) {
+    const int f = wave + 4 * i;  // fragment f: plane f / TM, tile f % TM
+    const int64_t tile = min(bm * TM + f % TM, cdiv<int64_t>(p.M, 16) - 1);
+    xsrc[i] = p.xh + (tile * p.KT + kt0) * 2048 + (f / TM) * 1024 + lane * 16;
+    xdst[i] = f * 1024;
+  }
+  // weight fragments of this wave (tiles past N clamped: columns >= N are never stored)
+  const int8_t* wsrc[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int64_t tile = min((n0 >> 4) + tn, cdiv<int64_t>(p.N, 16) - 1);
+    wsrc[tn] = p.wh + (tile * p.KT + kt0) * 2048 + lane * 16;
+  }
+
+  // The x copies are issued from inline asm: the compiler's wait-count pass cannot tell which
+  // stage a direct-to-LDS load writes, and with the builtin it drains every load in flight
+  // (weights included) once per unrolled loop trip. Only this code reads the ring, after the
+  // explicit s_waitcnt + s_barrier of each step. The asm has no register outputs; M0 (the
+  // LDS destination, wave-uniform) needs one wait state before the load that uses it.
+  auto issue_x = [&](int64_t step, int slot) {
+#pragma unroll
+    for (int i = 0; i < LX; ++i) {
+      const uint32_t lds = __builtin_amdgcn_readfirstlane(
+          (uint32_t)(uintptr_t)(lds_void_t*)(ring + slot * NFX * 1024 + xdst[i]));
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(xsrc[i] + step * 2048),
+                   "s"(lds)
+                   : "memory", "m0");
+    }
+  };
+  auto load_w = [&](int64_t step, v4i (&wb)[LW]) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      wb[2 * tn] = *reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048);
+      wb[2 * tn + 1] = *reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048 + 1024);
+    }
+  };
+
+  v4i hh[TM][TN], md[TM][TN], ll[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      hh[tm][tn] = v4i{0, 0, 0, 0};
+      md[tm][tn] = v4i{0, 0, 0, 0};
+      ll[tm][tn] = v4i{0, 0, 0, 0};
+    }
+
+  const int8_t* lds_lane = ring + lane * 16;
+  auto step = [&](int64_t j, v4i (&wb)[LW]) {
+    // lgkmcnt(0): this wave's reads of stage j-1 are complete before any wave refills it
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kWait) : "memory");
+    const int64_t nxt = j + R < nk ? j + R : nk - 1;
+    issue_x(nxt, (int)((j + R) % S));
+    const int8_t* stage = lds_lane + (int)(j % S) * NFX * 1024;
+    v4i xh[TM], xl[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      xh[tm] = *reinterpret_cast<const v4i*>(stage + tm * 1024);
+      xl[tm] = *reinterpret_cast<const v4i*>(stage + (TM + tm) * 1024);
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) hh[tm][tn] = mfma_i8(xh[tm], wb[2 * tn], hh[tm][tn]);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) md[tm][tn] = mfma_i8(xh[tm], wb[2 * tn + 1], md[tm][tn]);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) md[tm][tn] = mfma_i8(xl[tm], wb[2 * tn], md[tm][tn]);
+      if constexpr (!TRUNC) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) ll[tm][tn] = mfma_i8(xl[tm], wb[2 * tn + 1], ll[tm][tn]);
+      }
+    }
+    load_w(nxt, wb);
+  };
+
+  if (nk > 0) {
+    v4i w[R][LW];
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int64_t st = s < nk ? s : nk - 1;
+      issue_x(st, s);
+      load_w(st, w[s]);
+    }
+    int64_t j = 0;
+    for (; j + R <= nk; j += R) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) step(j + r, w[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r)
+      if (j + r < nk) step(j + r, w[r]);
+    // the repeated loads of the tail still target this workgroup's LDS and registers: drain them
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+
+  // Epilogue from registers: register r of lane holds C[4*(lane>>4) + r][lane & 15].
+  const int r16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + tm * 16 + kq * 4 + r;
+        const int64_t n = n0 + tn * 16 + r16;
+        if (m < p.M && n < p.N) {
+          int64_t tot = ((int64_t)hh[tm][tn][r] << 16) + ((int64_t)md[tm][tn][r] << 8);
+          if constexpr (!TRUNC) tot += (int64_t)ll[tm][tn][r];
+          exact_store(p, split, m, n, tot);
+        }
+      }
+}
+
+template <int BM, int WN, int R, bool TRUNC>
+hipError_t launch(const ExactParams& ep, hipStream_t st) {
+  const int64_t blocks = cdiv<int64_t>(ep.M, BM) * cdiv<int64_t>(ep.N, 4 * WN);
+  if (blocks > 0x7FFFFFFFLL || ep.sk > 65535) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((exact_xw_kernel<BM, WN, R, TRUNC>), dim3((unsigned)blocks, (unsigned)ep.sk), dim3(256), 0, st,
+                     ep);
+  return hipGetLastError();
+}
+
+// Instantiated (BM, WN, R); the 4-dot (F = 15) variants only where three accumulator sets fit.
+#define VXA_XW_TABLE(X)                                                                             \
+  X(32, 32, 4, 1) X(32, 64, 4, 1) X(64, 16, 4, 1) X(64, 32, 4, 1) X(64, 48, 4, 1) X(64, 64, 3, 1)   \
+  X(64, 64, 4, 0) X(128, 16, 4, 1) X(128, 32, 3, 1) X(128, 32, 4, 0) X(128, 48, 3, 0) X(128, 48, 4, 0)
+
+template <bool TRUNC>
+hipError_t dispatch(const ExactPlan& pl, const ExactParams& ep, hipStream_t st) {
+#define VXA_XW(BM_, WN_, R_, FOUR_)                                    \
+  if constexpr (TRUNC || FOUR_) {                                       \
+    if (pl.bm == BM_ && pl.bn == 4 * WN_ && pl.stages == R_)            \
+      return launch<BM_, WN_, R_, TRUNC>(ep, st);                       \
+  }
+  VXA_XW_TABLE(VXA_XW)
+#undef VXA_XW
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool exact_xw_supported(int bm, int bn, int r, bool trunc) {
+#define VXA_XW_HAS(BM_, WN_, R_, FOUR_) \
+  if (bm == BM_ && bn == 4 * WN_ && r == R_ && (trunc || FOUR_)) return true;
+  VXA_XW_TABLE(VXA_XW_HAS)
+#undef VXA_XW_HAS
+  return false;
+}
+
+hipError_t launch_exact_xw(const ExactPlan& pl, const ExactParams& ep, bool trunc, hipStream_t st) {
+  return trunc ? dispatch<true>(pl, ep, st) : dispatch<false>(pl, ep, st);
+}

@@ -72,6 +72,8 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
                 raise RuntimeError(f"config {cfg} changed the result (N={N} K={Kd} M={M})")
             t = time_graph(lambda i, c=cfg: run(i, c), rot)
             tried.append((t, cfg))
+            if len(tried) % 40 == 0:
+                print(f"  N={N} K={Kd} M={M}: {len(tried)} configs timed", file=sys.stderr, flush=True)
             if best is None or t < best[0]:
                 best = (t, cfg)
         wbs = [w.clone() for _ in range(rot)]
