@@ -56,7 +56,65 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
                     help="exact_int8 tuning table to use")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only launch the dominant GEMM (M=256 gate_up, table cfg) and a 1 GiB copy, --steps times "
+                         "each: the program rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs to measure HBM traffic")
     return ap.parse_args()
+
+
+TRAFFIC_SUMMARY = ROOT / "profiles" / "exact_gemm_m256_gate_up_hbm_traffic.md"
+
+
+def read_traffic(kernel_cfg):
+    """HBM bytes per launch of the dominant GEMM, as measured by the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes of `bench.py --profile-kernel` and recorded in TRAFFIC_SUMMARY (its
+    `traffic_bytes_per_launch` and `cfg` lines); None when no measurement matches this cfg."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    vals = {}
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("    ") and "=" in line:
+            k, v = line.strip().split("=", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        if json.loads(vals["cfg"]) != list(kernel_cfg):
+            return None
+        return int(vals["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def profile_kernel(args):
+    """Launch the dominant GEMM and a plain copy of known size --steps times each (counter runs)."""
+    import torch
+
+    from vllm_exact import _native
+    from vllm_exact import kernels as K
+    from vllm_exact import plugin
+
+    _native.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    plugin.load_table(args.table)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    M, (name, N, Kd) = 256, SHAPES[2]
+    cfg = plugin._cfg(M, N, Kd)
+    w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    wp, _, cw, sw = plugin.pack_weight(w)
+    x = torch.randn(M, Kd, device=dev, generator=gen).to(torch.bfloat16)
+    xd = K.digitize_packed(x, F)
+    out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    src = torch.randn(1 << 29, device=dev, generator=gen).to(torch.bfloat16)  # 1 GiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        K.exact_linear_packed(xd, (wp, cw, sw), Kd, F, TRUNC, out=out, cfg=cfg)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"gemm": f"M={M} {name} {N}x{Kd}", "cfg": list(cfg), "launches": args.steps,
+                      "copy_bytes": src.numel() * 2, "algorithmic_bytes": gemm_bytes(M, N, Kd)}), flush=True)
 
 
 def log(*a):
@@ -69,6 +127,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only: the exact linear path is a per-GPU kernel "
                                    "library (multi-GPU sharding is a design note); run with --gpus 1"}))
         sys.exit(2)
+    if args.profile_kernel:
+        profile_kernel(args)
+        return
     import numpy as np
     import torch
 
@@ -181,6 +242,7 @@ def main():
     else:
         roof = dict(bound="mfma", achieved=round(o / t_kernel / 1e6, 1), peak=INT8_PEAK_TOPS, unit="TFLOP/s",
                     frac=round(o / t_kernel / 1e6 / INT8_PEAK_TOPS, 4), traffic=None)
+    roof["traffic"] = read_traffic(cfg) if (M, name) == (256, "gate_up") else None
     roof.update(kernel=f"exact GEMM M={M} {name} {N}x{Kd} cfg={list(cfg)}", kernel_us=round(t_kernel, 2),
                 algorithmic_bytes=b, algorithmic_ops=o)
     log("roofline:", json.dumps(roof))
