@@ -106,6 +106,7 @@ def test_entry_points_validate_before_launching():
     assert call(H=24, KV=8) == nx.VXA_ERR_UNSUPPORTED  # G = 3
     assert call(split=1000) == nx.VXA_ERR_UNSUPPORTED
     assert call(blk=48) == nx.VXA_ERR_UNSUPPORTED
+    assert call(split=131072) == nx.VXA_ERR_UNSUPPORTED  # a segment's block-table entries must fit in LDS
     assert call(H=30, KV=8) == nx.VXA_ERR_ARG
     assert call(max_len=4096) == nx.VXA_ERR_WORKSPACE
     assert call(n=0) == nx.VXA_OK

@@ -73,17 +73,18 @@ __device__ inline void merge_ml(float& m, float& l, float ms, float ls) {
   m = mn;
 }
 
-__device__ inline int64_t page_offset(const PagedParams& p, int b, int key, int64_t sb, int64_t sp) {
-  int32_t blk, off;
-  if (p.bs_shift >= 0) {
-    blk = key >> p.bs_shift;
-    off = key & (p.bs - 1);
-  } else {
-    blk = (int32_t)((uint32_t)key / (uint32_t)p.bs);
-    off = key - blk * p.bs;
-  }
-  const int64_t page = p.bt[(int64_t)b * p.sbt + blk];
-  return page * sb + (int64_t)off * sp;
+__device__ inline int32_t page_of(const PagedParams& p, int key) {
+  return p.bs_shift >= 0 ? (key >> p.bs_shift) : (int32_t)((uint32_t)key / (uint32_t)p.bs);
+}
+
+// Element offset of `key`'s row in a cache with block stride sb and token stride sp. The
+// segment's block-table entries sit in LDS (pages[i] = block_table[b][blk0 + i]), so the K/V
+// address never waits on a global load of the table.
+__device__ inline int64_t page_offset(const PagedParams& p, const int32_t* pages, int blk0, int key, int64_t sb,
+                                      int64_t sp) {
+  const int32_t blk = page_of(p, key);
+  const int32_t off = key - blk * p.bs;
+  return (int64_t)pages[blk - blk0] * sb + (int64_t)off * sp;
 }
 
 template <int D>
@@ -116,6 +117,14 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
   const int start = s * p.split;
   if (start >= L) return;  // segment past the end: contributes exactly 0, never read
   const int end = min(start + p.split, L);
+
+  // The segment's block-table entries, staged once into LDS (dynamic shared memory sized
+  // split / bs + 2 entries by the launcher).
+  extern __shared__ int32_t s_pages[];
+  const int blk0 = page_of(p, start);
+  const int npg = page_of(p, end - 1) - blk0 + 1;
+  for (int i = threadIdx.x; i < npg; i += 64 * NW) s_pages[i] = p.bt[(int64_t)b * p.sbt + blk0 + i];
+  __syncthreads();
   const int ntile = (end - start + 15) >> 4;
   const int ngroup = (ntile + TPG - 1) / TPG;
 
@@ -148,7 +157,7 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
     for (int t = 0; t < TPG; ++t) {
       // K rows of this tile: lane col -> key, 8 dims per lane per step.
       const int key = min(kbase + 16 * t + col, end - 1);
-      const uint16_t* krow = p.kc + page_offset(p, b, key, p.skb, p.skp) + khead;
+      const uint16_t* krow = p.kc + page_offset(p, s_pages, blk0, key, p.skb, p.skp) + khead;
       v4f c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < QS; ++i) {
@@ -197,7 +206,7 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = min(kbase + 16 * t + 4 * row + j, end - 1);
-        const uint16_t* vrow = p.vc + page_offset(p, b, key, p.svb, p.svp) + vhead + col * DPL;
+        const uint16_t* vrow = p.vc + page_offset(p, s_pages, blk0, key, p.svb, p.svp) + vhead + col * DPL;
         float v[DPL];
         if constexpr (DPL == 4) {
           const uint2 raw = *reinterpret_cast<const uint2*>(vrow);
@@ -309,11 +318,15 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
   }
 }
 
+// LDS bytes of a segment's block-table entries (the pages a `split`-key window can touch).
+size_t page_table_bytes(int64_t split, int64_t bs) { return (size_t)(split / bs + 2) * sizeof(int32_t); }
+
 template <int D, int G, int TPG, int NW>
 hipError_t launch_partial(const PagedParams& pp, hipStream_t st) {
   const int64_t blocks = pp.n * pp.KV * pp.ns;
   if (blocks > 0x7FFFFFFFLL) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((paged_partial_kernel<D, G, TPG, NW>), dim3((unsigned)blocks), dim3(64 * NW), 0, st, pp);
+  hipLaunchKernelGGL((paged_partial_kernel<D, G, TPG, NW>), dim3((unsigned)blocks), dim3(64 * NW),
+                     page_table_bytes(pp.split, pp.bs), st, pp);
   return hipGetLastError();
 }
 
@@ -377,6 +390,7 @@ extern "C" int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh, const v
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return VXA_ERR_UNSUPPORTED;
   if (G != 1 && G != 2 && G != 4 && G != 8) return VXA_ERR_UNSUPPORTED;
   if (block_size > (1 << 30) || num_heads > (1 << 20)) return VXA_ERR_UNSUPPORTED;
+  if (page_table_bytes(split, block_size) > 32768) return VXA_ERR_UNSUPPORTED;  // split / block_size <= 8190
   // 16-byte row loads of q and V and 16/8-byte K fragments need aligned rows.
   if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 || sqt % 8 || sqh % 8 ||
       skb % 8 || skp % 8 || skh % 8 || svb % 8 || svp % 8 || svh % 8)

@@ -20,8 +20,11 @@ import torch
 
 from . import _native as _nx
 
-SPLIT = 1024
-BLK = 64
+# gfx950 defaults, measured at H32/KV8/D128/BS16 (64x8K, 16x16K, 256x1K): one 16-key tile per
+# wave step keeps the kernel at 4 waves per SIMD, and 2048-key segments keep enough
+# workgroups in flight at 16x16K.
+SPLIT = 2048
+BLK = 16
 WARPS = 4
 STAGES = 1
 MAX_LEN = 16384  # fixes the number of segments; enable() sets it to max_model_len
