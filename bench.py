@@ -1,6 +1,7 @@
 """Benchmark of the exact linear path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-attention] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-attention] [--no-decode-step] [--no-cpu]
+    python bench.py --profile-kernel [--steps K]   (launches for rocprofv3 counter runs)
 
 Step: one pass of the decode-shaped exact linear sweep (the BASELINE workload for this
 metric): QKV 4096->6144, O 4096->4096, gate_up 4096->24576 and down 12288->4096 at
@@ -15,6 +16,10 @@ Also reported, from the same run:
 * `roofline` of the dominant kernel (the GEMM launch with the largest share of the step),
   timed alone with HIP events on its own stream;
 * split-bf16 paged decode attention at H=32/KV=8/D=128/BS=16 for 64x8K, 16x16K, 256x1K (TB/s);
+* `decode_step`: the synthetic decode step of the ~9B hybrid (32 layers of the four exact
+  linears, paged attention on 8 of them, exact lm_head 4096->151936) at batch/context 256/1K,
+  64/8K and 16/16K: ms per step as a HIP graph, the same step with hipBLASLt bf16 linears,
+  bitwise batch invariance of the logits, and a CPU estimate from the oracle's timings;
 * bit-exactness of the benchmarked outputs against the CPU oracle (sampled rows);
 * `cpu_baseline`: the C oracle (OpenMP) on a bounded sample of the same sweep, extrapolated
   per op, on this host's cores.
@@ -36,6 +41,75 @@ SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("do
 MS = [1, 16, 64, 256]
 F, TRUNC, NDOTS = 14, True, 3
 ATTN_CASES = [(64, 8192), (16, 16384), (256, 1024)]
+DECODE_CASES = [(256, 1024), (64, 8192), (16, 16384)]  # (batch, context) of the decode-step emulation
+HIDDEN, VOCAB, LAYERS, ATTN_EVERY = 4096, 151936, 32, 4
+ATT_H, ATT_KV, ATT_D, ATT_BS = 32, 8, 128, 16
+
+
+class DecodeStep:
+    """Synthetic decode step of the ~9B hybrid with random-init weights (the GDN recurrence
+    excluded): LAYERS layers of the four exact linears, paged decode attention on every
+    ATTN_EVERY-th layer (8 of 32), and the exact lm_head. Non-attention layers pass the q
+    slice of the QKV output on as the mixer output. Between linears: residual adds, SiLU-gated
+    MLP, and a per-row power-of-two rescale (exact, so every op is row-local and batch
+    invariant). `exact=False` runs the same step with hipBLASLt bf16 matmuls for the linears
+    (same attention kernel): the non-exact baseline."""
+
+    def __init__(self, torch, plugin, P, dev, gen, layers=LAYERS, vocab=VOCAB, keep_bf16=True):
+        self.torch, self.P, self.dev = torch, P, dev
+        self.layers = []
+        for _ in range(layers):
+            ws = {}
+            for name, N, Kd in SHAPES:
+                w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+                ws[name] = (plugin.pack_weight(w), w if keep_bf16 else None)
+            self.layers.append(ws)
+        w = (torch.randn(vocab, HIDDEN, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        self.lm = (plugin.pack_weight(w), w if keep_bf16 else None)
+        self.digit_bytes = sum(2 * N * Kd for _, N, Kd in SHAPES) * layers + 2 * vocab * HIDDEN
+
+    def kv(self, B, L, gen):
+        torch = self.torch
+        nbp = -(-L // ATT_BS)
+        caches = []
+        n_att = sum(1 for i in range(len(self.layers)) if i % ATTN_EVERY == ATTN_EVERY - 1)
+        for _ in range(n_att):
+            kv = torch.randn(B * nbp, ATT_KV, ATT_BS, 2 * ATT_D, device=self.dev, generator=gen,
+                             dtype=torch.bfloat16)
+            kc, vc = kv.transpose(1, 2).split(ATT_D, dim=-1)
+            caches.append((kv, kc, vc))
+        bt = torch.randperm(B * nbp, device=self.dev, generator=gen).view(B, nbp).to(torch.int32)
+        sl = torch.full((B,), L, device=self.dev, dtype=torch.int32)
+        return caches, bt, sl
+
+    def step(self, h, caches, bt, sl, exact=True):
+        torch = self.torch
+        B = h.shape[0]
+
+        def lin(x, wp):
+            return torch.ops.exactmm.linear(x, *wp[0]) if exact else torch.matmul(x, wp[1].T)
+
+        def rownorm(t):  # t * 2^-e, e = frexp exponent of the row absmax: exact and row-local
+            e = torch.frexp(t.abs().amax(dim=-1, keepdim=True).float()).exponent
+            return torch.ldexp(t.float(), -e).to(torch.bfloat16)
+
+        a = 0
+        for i, ws in enumerate(self.layers):
+            qkv = lin(rownorm(h), ws["qkv"])
+            if i % ATTN_EVERY == ATTN_EVERY - 1:
+                _, kc, vc = caches[a]
+                a += 1
+                o = torch.empty(B, ATT_H, ATT_D, device=h.device, dtype=torch.bfloat16)
+                self.P.paged_decode(qkv[:, :HIDDEN].view(B, ATT_H, ATT_D), kc, vc, bt, sl, ATT_D ** -0.5, o, B,
+                                    self.P.MAX_LEN)
+                mix = o.view(B, HIDDEN)
+            else:
+                mix = qkv[:, :HIDDEN]
+            h = h + lin(mix, ws["o"])
+            gu = lin(rownorm(h), ws["gate_up"])
+            half = gu.shape[1] // 2
+            h = h + lin(torch.nn.functional.silu(gu[:, :half]) * gu[:, half:], ws["down"])
+        return lin(rownorm(h), self.lm)
 
 
 def gemm_bytes(M, N, K):
@@ -53,6 +127,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode-step", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
                     help="exact_int8 tuning table to use")
@@ -287,6 +362,62 @@ def main():
             del kv, kc, vc
             torch.cuda.empty_cache()
 
+    # ---------------------------------------------------------------- decode-step emulation
+    decode = []
+    if not args.no_decode_step:
+        P.MAX_LEN = 16384
+        model = DecodeStep(torch, plugin, P, dev, gen)
+        log(f"decode-step model: {model.digit_bytes / 1e9:.2f} GB of weight digits")
+        for B, L in DECODE_CASES:
+            caches, bt, sl = model.kv(B, L, gen)
+            h0 = torch.randn(B, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
+            rec = dict(B=B, L=L)
+            full = None
+            for exact in (True, False):
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    model.step(h0, caches, bt, sl, exact)
+                torch.cuda.current_stream().wait_stream(side)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    logits = model.step(h0, caches, bt, sl, exact)
+                for _ in range(2):
+                    g.replay()
+                torch.cuda.synchronize()
+                ts = []
+                for _ in range(10):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    g.replay()
+                    e1.record()
+                    e1.synchronize()
+                    ts.append(e0.elapsed_time(e1))
+                rec["exact_ms" if exact else "bf16_hipblaslt_ms"] = round(float(np.median(ts)), 3)
+                if exact:
+                    full = logits.clone()
+                del g, logits
+                torch.cuda.synchronize()
+            # bitwise batch invariance of the exact logits: first and last request alone, and
+            # the two of them as a batch in reversed order
+            ok = True
+            for i in (0, B - 1):
+                ok &= torch.equal(model.step(h0[i:i + 1], caches, bt[i:i + 1], sl[i:i + 1]), full[i:i + 1])
+            sel = torch.tensor([B - 1, 0], device=dev)
+            ok &= torch.equal(model.step(h0[sel], caches, bt[sel].contiguous(), sl[sel].contiguous()), full[sel])
+            kv_bytes = len(caches) * B * L * ATT_KV * ATT_D * 2 * 2
+            floor_ms = (model.digit_bytes + kv_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
+            rec.update(ratio_exact_vs_bf16=round(rec["exact_ms"] / rec["bf16_hipblaslt_ms"], 3),
+                       logits_batch_invariant=bool(ok), hbm_floor_ms=round(floor_ms, 3),
+                       exact_hbm_frac=round(floor_ms / rec["exact_ms"], 3))
+            decode.append(rec)
+            log(json.dumps(rec))
+            del caches, bt, sl, full
+            torch.cuda.empty_cache()
+        del model
+        torch.cuda.empty_cache()
+
     # ---------------------------------------------------------------- CPU baseline (oracle, sampled)
     cpu = None
     if not args.no_cpu:
@@ -297,7 +428,7 @@ def main():
             ns = min(N, 2048)
             w = (rng.standard_normal((ns, Kd)) * 0.02).astype(np.float32)
             samples[name] = (ns, oracle.digitize_c(w, F))
-        total_s, sample_desc = 0.0, []
+        total_s, sample_desc, cpu_op_s = 0.0, [], {}
         min_s = args.cpu_seconds / len(ops)
         for M, name, N, Kd in ops:
             ns, wd = samples[name]
@@ -311,12 +442,32 @@ def main():
                 if reps * dt >= min_s / 4 or reps >= 50:
                     break
             total_s += dt * N / ns
+            cpu_op_s[(M, name)] = dt * N / ns
             sample_desc.append(f"M={M} {name} {ns}/{N} rows x{reps}")
         cpu = dict(value=round(step_bytes / total_s / 1e9, 3), unit="GB/s", cores=threads, kind="port",
                    sample="C oracle (digitize + exact integer digit dots, OpenMP) on the first rows of every op "
                           "of the sweep, time extrapolated linearly in N: " + "; ".join(sample_desc),
                    step_ms_extrapolated=round(total_s * 1e3, 1))
         log("cpu baseline:", json.dumps(cpu))
+        if decode:
+            # decode step on the CPU, extrapolated: the sampled per-op linear times at M = B,
+            # lm_head scaled from QKV by N, attention from a timed fp64 oracle sample
+            Ls = 1024
+            qs = rng.standard_normal((1, ATT_H, ATT_D)).astype(np.float32)
+            cache = rng.standard_normal((Ls // ATT_BS, ATT_BS, ATT_KV, ATT_D)).astype(np.float32)
+            to_bits = lambda a: (a.view(np.uint32) >> 16).astype(np.uint16)
+            bt_s = np.arange(Ls // ATT_BS, dtype=np.int32).reshape(1, -1)
+            sl_s = np.array([Ls], np.int32)
+            t0 = time.perf_counter()
+            oracle.paged_decode_c(to_bits(qs), to_bits(cache), to_bits(cache), bt_s, sl_s, ATT_D ** -0.5, 1)
+            att_key_s = (time.perf_counter() - t0) / Ls
+            for rec in decode:
+                B = rec["B"]
+                lin_s = LAYERS * sum(cpu_op_s[(B, name)] for name, _, _ in SHAPES)
+                lm_s = cpu_op_s[(B, "qkv")] * VOCAB / 6144
+                att_s = (LAYERS // ATTN_EVERY) * B * rec["L"] * att_key_s
+                rec["cpu_ms_extrapolated"] = round((lin_s + lm_s + att_s) * 1e3, 1)
+            log("decode step cpu:", json.dumps([(r["B"], r["L"], r["cpu_ms_extrapolated"]) for r in decode]))
 
     result = {
         "metric": METRIC,
@@ -341,6 +492,7 @@ def main():
         "bit_exact": exact_ok,
         "per_op": per_op,
         "attention": attn,
+        "decode_step": decode,
     }
     print(json.dumps(result), flush=True)
 
