@@ -28,11 +28,13 @@ SPLITS = (1, 2, 4)
 
 
 def candidates(M, Kd):
-    """Every instantiated kernel shape whose M block does not exceed max(16, next_pow2(M)),
-    times the split-K factors (kernels.py:298 filters the same way)."""
+    """Every instantiated kernel shape whose M block does not exceed max(16, next_pow2(M))
+    (kernels.py:298 filters the same way; the 32-row x-through-LDS tiles are kept for every M),
+    times the split-K factors."""
     out = []
     for c in K.EXACT_CFGS:
-        if c[0] > max(16, 1 << max(0, (M - 1).bit_length())):
+        xw32 = c[2] == 64 and c[0] == 32  # the 32-row x-through-LDS tiles also serve M <= 16
+        if c[0] > max(16, 1 << max(0, (M - 1).bit_length())) and not xw32:
             continue
         if M <= 16 and c[0] >= 64 and c[4] >= 2:
             continue  # the LDS-ring kernel needs a real M tile
