@@ -58,8 +58,8 @@ int lds_stages(int bm, int bn, int want) {
 }
 
 // cfg tuple (BM, BN, BK, warps, stages, GM[, SK[, mma]]) -> kernel family and shape:
-//   BK == 64, warps == 4: on packed operands, the x-through-LDS kernel with tile BM x BN and
-//     R = stages weight register sets when instantiated (exact_xw_supported); otherwise, and
+//   BK == 64, warps 4 or 8: on packed operands, the x-through-LDS kernel with tile BM x BN,
+//     R = stages weight register sets and `warps` waves when instantiated (exact_xw_supported); otherwise, and
 //     on row-major digits, the LDS-ring kernel below with BM and BN clamped to 64..128;
 //   BM >= 64, BN >= 64, warps == 4, stages >= 2: LDS-ring kernel with tile
 //     min(BM,128) x min(BN,128) and `stages` ring stages (clamped to instantiated depths);
@@ -75,11 +75,12 @@ int make_plan(int64_t K, const int32_t* cfg, int cfg_len, ExactPlan* out) {
   const int32_t SKr = cfg_len > 6 ? cfg[6] : 1;
   if (BM <= 0 || BN <= 0 || BK <= 0 || warps <= 0 || stages <= 0 || SKr <= 0) return VXA_ERR_ARG;
   ExactPlan p = {};
-  if (BK == 64 && warps == 4) {
+  if (BK == 64 && (warps == 4 || warps == 8)) {
     p.family = kFamilyXw;
     p.bm = BM;
     p.bn = BN;
     p.stages = stages;
+    p.nwk = warps;
   } else if (BM >= 64 && BN >= 64 && warps == 4 && stages >= 2) {
     p.family = kFamilyLds;
     p.bm = BM >= 128 ? 128 : 64;
@@ -134,7 +135,7 @@ int run_exact(const ExactPlan& pl, ExactParams& ep, int trunc, bool packed, bool
     dim3 grid((unsigned)cdiv<int64_t>(ep.N, 256), (unsigned)ep.M, (unsigned)pl.sk);
     hipLaunchKernelGGL(exact_scalar_kernel, grid, dim3(256), 0, st, ep, trunc);
     err = hipGetLastError();
-  } else if (pl.family == kFamilyXw && packed && exact_xw_supported(pl.bm, pl.bn, pl.stages, trunc != 0)) {
+  } else if (pl.family == kFamilyXw && packed && exact_xw_supported(pl.bm, pl.bn, pl.stages, pl.nwk, trunc != 0)) {
     err = launch_exact_xw(pl, ep, trunc != 0, st);
   } else if (pl.family == kFamilyXw || pl.family == kFamilyLds) {
     ExactPlan lp = pl;

@@ -43,7 +43,7 @@ struct ExactPlan {
   // C 64-wide K steps whose loads are issued together
   int mt, nt, nwk, chunk;
   // LDS pipeline kernel: BM x BN workgroup tile, S ring stages; x-through-LDS kernel:
-  // BM x BN workgroup tile, `stages` = R weight register sets
+  // BM x BN workgroup tile, `stages` = R weight register sets, `nwk` = 4 or 8 waves
   int bm, bn, stages;
   int64_t kch;
   int32_t sk;
@@ -93,4 +93,4 @@ hipError_t launch_exact_lds(const ExactPlan& pl, const ExactParams& ep, bool tru
 bool exact_small_supported(int mt, int nt, int chunk, int nwk);
 // Packed operands only (exact_gemm_xw.hip).
 hipError_t launch_exact_xw(const ExactPlan& pl, const ExactParams& ep, bool trunc, hipStream_t st);
-bool exact_xw_supported(int bm, int bn, int r, bool trunc);
+bool exact_xw_supported(int bm, int bn, int r, int waves, bool trunc);

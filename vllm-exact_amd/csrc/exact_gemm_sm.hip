@@ -68,13 +68,18 @@ __global__ __launch_bounds__(64 * NWK) void exact_sm_kernel(ExactParams p) {
     }
   }
 
-  v4i hh[MT][NT], md[MT][NT], ll[MT][NT];
+  // With one or two tiles the two cross terms get accumulators of their own (mx for xl*wh),
+  // so consecutive MFMAs never depend on each other; with more tiles one accumulator each,
+  // updated in passes over all tiles.
+  constexpr bool kSplitMd = MT * NT <= 2;
+  v4i hh[MT][NT], md[MT][NT], mx[MT][NT], ll[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       hh[mt][nt] = v4i{0, 0, 0, 0};
       md[mt][nt] = v4i{0, 0, 0, 0};
+      mx[mt][nt] = v4i{0, 0, 0, 0};
       ll[mt][nt] = v4i{0, 0, 0, 0};
     }
 
@@ -104,12 +109,24 @@ __global__ __launch_bounds__(64 * NWK) void exact_sm_kernel(ExactParams p) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
+          for (int nt = 0; nt < NT; ++nt) hh[mt][nt] = mfma_i8(ah[c][mt], bh[c][nt], hh[mt][nt]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) md[mt][nt] = mfma_i8(ah[c][mt], bl[c][nt], md[mt][nt]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
-            hh[mt][nt] = mfma_i8(ah[c][mt], bh[c][nt], hh[mt][nt]);
-            md[mt][nt] = mfma_i8(ah[c][mt], bl[c][nt], md[mt][nt]);
-            md[mt][nt] = mfma_i8(al[c][mt], bh[c][nt], md[mt][nt]);
-            if constexpr (!TRUNC) ll[mt][nt] = mfma_i8(al[c][mt], bl[c][nt], ll[mt][nt]);
+            if constexpr (kSplitMd) mx[mt][nt] = mfma_i8(al[c][mt], bh[c][nt], mx[mt][nt]);
+            else md[mt][nt] = mfma_i8(al[c][mt], bh[c][nt], md[mt][nt]);
           }
+        if constexpr (!TRUNC) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) ll[mt][nt] = mfma_i8(al[c][mt], bl[c][nt], ll[mt][nt]);
+        }
       }
     }
   }
@@ -122,7 +139,9 @@ __global__ __launch_bounds__(64 * NWK) void exact_sm_kernel(ExactParams p) {
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        int64_t tot = ((int64_t)hh[mt][nt][r] << 16) + ((int64_t)md[mt][nt][r] << 8);
+        int64_t cross = (int64_t)md[mt][nt][r];
+        if constexpr (kSplitMd) cross += (int64_t)mx[mt][nt][r];
+        int64_t tot = ((int64_t)hh[mt][nt][r] << 16) + (cross << 8);
         if constexpr (!TRUNC) tot += (int64_t)ll[mt][nt][r];
         if (NWK == 1) {
           red[(mt * 16 + kq * 4 + r) * BN + nt * 16 + r16] = (unsigned long long)tot;

@@ -26,22 +26,26 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int BM, int WN, int R, bool TRUNC>
-__global__ __launch_bounds__(256) void exact_xw_kernel(ExactParams p) {
-  constexpr int TM = BM / 16;     // 16-row tiles of x
+template <int BM, int WN, int R, int WMS, bool TRUNC>
+__global__ __launch_bounds__(256 * WMS) void exact_xw_kernel(ExactParams p) {
+  constexpr int NWAVE = 4 * WMS;  // waves: 4 along N times WMS along M
+  constexpr int TMA = BM / 16;    // 16-row tiles of the x tile
+  constexpr int TM = TMA / WMS;   // ... of one wave
   constexpr int TN = WN / 16;     // 16-column tiles of one wave
   constexpr int BN = 4 * WN;      // workgroup tile width
   constexpr int S = R + 1;        // x ring stages
-  constexpr int NFX = 2 * TM;     // x fragments per stage (h and l planes)
-  constexpr int LX = NFX / 4;     // x fragments each wave loads per stage
+  constexpr int NFX = 2 * TMA;    // x fragments per stage (h and l planes)
+  constexpr int LX = NFX / NWAVE; // x fragments each wave loads per stage
   constexpr int LW = 2 * TN;      // weight fragments each wave loads per step
   constexpr int kWait = (R - 1) * (LX + LW);
-  static_assert(NFX % 4 == 0, "x fragments split evenly over the 4 waves");
+  static_assert(TMA % WMS == 0 && NFX % NWAVE == 0, "x fragments split evenly over the waves");
   static_assert(kWait <= 63, "vmcnt limit");
   __shared__ __attribute__((aligned(1024))) int8_t ring[S * NFX * 1024];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int wn = wave & 3;   // column block of this wave
+  const int wm = wave >> 2;  // row block of this wave (WMS > 1)
 
   // Logical tile order: M tiles fastest, then N tiles, then K splits; the workgroups that
   // share one weight tile are neighbours and, through xcd_swizzle, on one XCD.
@@ -51,8 +55,8 @@ __global__ __launch_bounds__(256) void exact_xw_kernel(ExactParams p) {
   const int64_t bm = t % nbm;
   const int64_t bn = (t / nbm) % nbn;
   const int split = (int)(t / (nbm * nbn));
-  const int64_t m0 = bm * BM;
-  const int64_t n0 = bn * BN + wave * WN;
+  const int64_t m0 = bm * BM + wm * (BM / WMS);
+  const int64_t n0 = bn * BN + wn * WN;
   const int64_t kb = (int64_t)split * p.kch;
   const int64_t ke = min(kb + p.kch, p.kpad);
   const int64_t nk = (ke - kb) >> 6;
@@ -63,9 +67,9 @@ __global__ __launch_bounds__(256) void exact_xw_kernel(ExactParams p) {
   int xdst[LX];
 #pragma unroll
   for (int i = 0; i < LX; ++i) {
-    const int f = wave + 4 * i;  // fragment f: plane f / TM, tile f % TM
-    const int64_t tile = min(bm * TM + f % TM, cdiv<int64_t>(p.M, 16) - 1);
-    xsrc[i] = p.xh + (tile * p.KT + kt0) * 2048 + (f / TM) * 1024 + lane * 16;
+    const int f = wave + NWAVE * i;  // fragment f: plane f / TMA, tile f % TMA
+    const int64_t tile = min(bm * TMA + f % TMA, cdiv<int64_t>(p.M, 16) - 1);
+    xsrc[i] = p.xh + (tile * p.KT + kt0) * 2048 + (f / TMA) * 1024 + lane * 16;
     xdst[i] = f * 1024;
   }
   // weight fragments of this wave (tiles past N clamped: columns >= N are never stored)
@@ -119,21 +123,28 @@ __global__ __launch_bounds__(256) void exact_xw_kernel(ExactParams p) {
     v4i xh[TM], xl[TM];
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
-      xh[tm] = *reinterpret_cast<const v4i*>(stage + tm * 1024);
-      xl[tm] = *reinterpret_cast<const v4i*>(stage + (TM + tm) * 1024);
+      xh[tm] = *reinterpret_cast<const v4i*>(stage + (wm * TM + tm) * 1024);
+      xl[tm] = *reinterpret_cast<const v4i*>(stage + (TMA + wm * TM + tm) * 1024);
     }
+    // One pass per digit product over all tiles: the two updates of an `md` accumulator are
+    // TM * TN MFMAs apart, so no MFMA waits for the result of the one before it.
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
+    for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) hh[tm][tn] = mfma_i8(xh[tm], wb[2 * tn], hh[tm][tn]);
 #pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
       for (int tn = 0; tn < TN; ++tn) md[tm][tn] = mfma_i8(xh[tm], wb[2 * tn + 1], md[tm][tn]);
 #pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
       for (int tn = 0; tn < TN; ++tn) md[tm][tn] = mfma_i8(xl[tm], wb[2 * tn], md[tm][tn]);
-      if constexpr (!TRUNC) {
+    if constexpr (!TRUNC) {
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) ll[tm][tn] = mfma_i8(xl[tm], wb[2 * tn + 1], ll[tm][tn]);
-      }
     }
     load_w(nxt, wb);
   };
@@ -176,26 +187,29 @@ __global__ __launch_bounds__(256) void exact_xw_kernel(ExactParams p) {
       }
 }
 
-template <int BM, int WN, int R, bool TRUNC>
+template <int BM, int WN, int R, int WMS, bool TRUNC>
 hipError_t launch(const ExactParams& ep, hipStream_t st) {
   const int64_t blocks = cdiv<int64_t>(ep.M, BM) * cdiv<int64_t>(ep.N, 4 * WN);
   if (blocks > 0x7FFFFFFFLL || ep.sk > 65535) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((exact_xw_kernel<BM, WN, R, TRUNC>), dim3((unsigned)blocks, (unsigned)ep.sk), dim3(256), 0, st,
-                     ep);
+  hipLaunchKernelGGL((exact_xw_kernel<BM, WN, R, WMS, TRUNC>), dim3((unsigned)blocks, (unsigned)ep.sk),
+                     dim3(256 * WMS), 0, st, ep);
   return hipGetLastError();
 }
 
-// Instantiated (BM, WN, R); the 4-dot (F = 15) variants only where three accumulator sets fit.
-#define VXA_XW_TABLE(X)                                                                             \
-  X(32, 32, 4, 1) X(32, 64, 4, 1) X(64, 16, 4, 1) X(64, 32, 4, 1) X(64, 48, 4, 1) X(64, 64, 3, 1)   \
-  X(64, 64, 4, 0) X(128, 16, 4, 1) X(128, 32, 3, 1) X(128, 32, 4, 0) X(128, 48, 3, 0) X(128, 48, 4, 0)
+// Instantiated (BM, WN, R, WMS); the 4-dot (F = 15) variants only where three accumulator
+// sets fit. WMS = 2 runs 8 waves (two per SIMD), each on half of the BM rows.
+#define VXA_XW_TABLE(X)                                                                                   \
+  X(32, 32, 4, 1, 1) X(32, 64, 4, 1, 1) X(64, 16, 4, 1, 1) X(64, 32, 4, 1, 1) X(64, 48, 4, 1, 1)          \
+  X(64, 64, 3, 1, 1) X(64, 64, 4, 1, 0) X(128, 16, 4, 1, 1) X(128, 32, 3, 1, 1) X(128, 32, 4, 1, 0)       \
+  X(128, 48, 3, 1, 0) X(128, 48, 4, 1, 0) X(64, 32, 4, 2, 1) X(64, 48, 4, 2, 1) X(64, 64, 4, 2, 0)        \
+  X(128, 32, 4, 2, 1) X(128, 48, 3, 2, 0) X(128, 48, 4, 2, 0) X(128, 64, 2, 2, 0)
 
 template <bool TRUNC>
 hipError_t dispatch(const ExactPlan& pl, const ExactParams& ep, hipStream_t st) {
-#define VXA_XW(BM_, WN_, R_, FOUR_)                                    \
-  if constexpr (TRUNC || FOUR_) {                                       \
-    if (pl.bm == BM_ && pl.bn == 4 * WN_ && pl.stages == R_)            \
-      return launch<BM_, WN_, R_, TRUNC>(ep, st);                       \
+#define VXA_XW(BM_, WN_, R_, WMS_, FOUR_)                                                  \
+  if constexpr (TRUNC || FOUR_) {                                                           \
+    if (pl.bm == BM_ && pl.bn == 4 * WN_ && pl.stages == R_ && pl.nwk == 4 * WMS_)          \
+      return launch<BM_, WN_, R_, WMS_, TRUNC>(ep, st);                                     \
   }
   VXA_XW_TABLE(VXA_XW)
 #undef VXA_XW
@@ -204,9 +218,9 @@ hipError_t dispatch(const ExactPlan& pl, const ExactParams& ep, hipStream_t st) 
 
 }  // namespace
 
-bool exact_xw_supported(int bm, int bn, int r, bool trunc) {
-#define VXA_XW_HAS(BM_, WN_, R_, FOUR_) \
-  if (bm == BM_ && bn == 4 * WN_ && r == R_ && (trunc || FOUR_)) return true;
+bool exact_xw_supported(int bm, int bn, int r, int waves, bool trunc) {
+#define VXA_XW_HAS(BM_, WN_, R_, WMS_, FOUR_) \
+  if (bm == BM_ && bn == 4 * WN_ && r == R_ && waves == 4 * WMS_ && (trunc || FOUR_)) return true;
   VXA_XW_TABLE(VXA_XW_HAS)
 #undef VXA_XW_HAS
   return false;
