@@ -83,6 +83,8 @@ __global__ __launch_bounds__(64 * NWK) void exact_sm_kernel(ExactParams p) {
       ll[mt][nt] = v4i{0, 0, 0, 0};
     }
 
+  // One M tile covering all rows reads each weight fragment once: stream it (non-temporal).
+  const bool stream_w = cdiv<int64_t>(p.M, BM) == 1;
   const int64_t nsteps = (ke - kb) >> 6;
   for (int64_t s0 = wave; s0 < nsteps; s0 += (int64_t)NWK * C) {
     v4i ah[C][MT], al[C][MT], bh[C][NT], bl[C][NT];
@@ -93,8 +95,13 @@ __global__ __launch_bounds__(64 * NWK) void exact_sm_kernel(ExactParams p) {
         const int64_t off = s * kStep;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          bh[c][nt] = *reinterpret_cast<const v4i*>(whp[nt] + off);
-          bl[c][nt] = *reinterpret_cast<const v4i*>(wlp[nt] + off);
+          if (stream_w) {
+            bh[c][nt] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(whp[nt] + off));
+            bl[c][nt] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wlp[nt] + off));
+          } else {
+            bh[c][nt] = *reinterpret_cast<const v4i*>(whp[nt] + off);
+            bl[c][nt] = *reinterpret_cast<const v4i*>(wlp[nt] + off);
+          }
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {

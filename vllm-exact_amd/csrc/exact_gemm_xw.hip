@@ -100,11 +100,23 @@ __global__ __launch_bounds__(256 * WMS) void exact_xw_kernel(ExactParams p) {
                    : "memory", "m0");
     }
   };
+  // When one M tile covers all rows, each weight fragment is read by this workgroup alone:
+  // stream it with non-temporal loads. Otherwise the workgroups of the other M tiles read the
+  // same fragments at about the same time (xcd_swizzle) and should find them in L2.
+  const bool stream_w = nbm == 1;
   auto load_w = [&](int64_t step, v4i (&wb)[LW]) {
+    if (stream_w) {
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      wb[2 * tn] = *reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048);
-      wb[2 * tn + 1] = *reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048 + 1024);
+      for (int tn = 0; tn < TN; ++tn) {
+        wb[2 * tn] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048));
+        wb[2 * tn + 1] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048 + 1024));
+      }
+    } else {
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        wb[2 * tn] = *reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048);
+        wb[2 * tn + 1] = *reinterpret_cast<const v4i*>(wsrc[tn] + step * 2048 + 1024);
+      }
     }
   };
 
