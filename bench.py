@@ -16,6 +16,8 @@ Also reported, from the same run:
 * `roofline` of the dominant kernel (the GEMM launch with the largest share of the step),
   timed alone with HIP events on its own stream;
 * split-bf16 paged decode attention at H=32/KV=8/D=128/BS=16 for 64x8K, 16x16K, 256x1K (TB/s);
+* `lm_head`: the exact lm_head 4096->151936 at M = 16 and 256 with per-row activation scales
+  10^U(-2,2) (full op time, roofline fractions, bit-exactness on sampled rows);
 * `decode_step`: the synthetic decode step of the ~9B hybrid (32 layers of the four exact
   linears, paged attention on 8 of them, exact lm_head 4096->151936) at batch/context 256/1K,
   64/8K and 16/16K: ms per step as a HIP graph, the same step with hipBLASLt bf16 linears,
@@ -128,6 +130,7 @@ def parse():
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode-step", action="store_true")
+    ap.add_argument("--no-lm-head", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
                     help="exact_int8 tuning table to use")
@@ -362,6 +365,33 @@ def main():
             del kv, kc, vc
             torch.cuda.empty_cache()
 
+    # ---------------------------------------------------------------- exact lm_head (config 3)
+    lm_head = []
+    if not args.no_lm_head:
+        N, Kd = VOCAB, HIDDEN
+        w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        lw = [plugin.pack_weight(w) for _ in range(2)]
+        for M in (16, 256):
+            # activations N(0,1) scaled per row by 10^U(-2,2): mixed magnitudes through the epilogue
+            scale = 10.0 ** (torch.rand(M, 1, device=dev, generator=gen) * 4 - 2)
+            x = (torch.randn(M, Kd, device=dev, generator=gen) * scale).to(torch.bfloat16)
+            t = time_graph(lambda r: torch.ops.exactmm.linear(x, *lw[r]), 2, calls_per_replay=4, replays=10)
+            b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
+            y = torch.ops.exactmm.linear(x, *lw[0])
+            # bit-exactness on sampled rows and the first 4096 vocabulary rows
+            rows = np.array([0, M // 2, M - 1])
+            wd = oracle.digitize_c(w[:4096].float().cpu().numpy(), F)
+            xdn = oracle.digitize_c(x.float().cpu().numpy()[rows], F)
+            want = oracle.bf16_rne_c(oracle.exact_linear_c(xdn, wd, F, TRUNC)).reshape(len(rows), 4096)
+            got = y[rows.tolist(), :4096].cpu().view(torch.int16).numpy().view(np.uint16)
+            rec = dict(M=M, N=N, K=Kd, op_us=round(t, 2), GBps=round(b / t / 1e3, 1), hbm_frac=round(b / t / 1e3 / HBM_PEAK_GBS, 3),
+                       TOPS=round(o / t / 1e6, 1), mfma_frac=round(o / t / 1e6 / INT8_PEAK_TOPS, 3),
+                       cfg=list(plugin._cfg(M, N, Kd)), bit_exact=bool(np.array_equal(got, want)))
+            lm_head.append(rec)
+            log(json.dumps(rec))
+        del w, lw
+        torch.cuda.empty_cache()
+
     # ---------------------------------------------------------------- decode-step emulation
     decode = []
     if not args.no_decode_step:
@@ -492,6 +522,7 @@ def main():
         "bit_exact": exact_ok,
         "per_op": per_op,
         "attention": attn,
+        "lm_head": lm_head,
         "decode_step": decode,
     }
     print(json.dumps(result), flush=True)
