@@ -46,6 +46,41 @@ def test_shipped_table_is_well_formed():
             assert int(m) > 0 and 7 <= len(cfg) <= 8
     plugin.load_table(path)
     plugin.load_table(None)
+    # every entry names an instantiated kernel: x-through-LDS tiles (BK = 64) exactly, the
+    # other families through the plan's nearest-instantiation rule
+    xw = {(bm, 4 * wn, r, nw) for bm, wn, r, nw in K.XW_SHAPES}
+    for row in raw.values():
+        for cfg in row.values():
+            if cfg[2] == 64:
+                assert (cfg[0], cfg[1], cfg[4], cfg[3]) in xw, cfg
+
+
+def test_bench_traffic_summary_matches_the_table():
+    # bench.py reports roofline.traffic from the rocprofv3 FETCH/WRITE summary only when it
+    # was measured with the cfg the table now gives the dominant GEMM (M = 256 gate_up)
+    import importlib.util
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("bench_mod", root / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    plugin.load_table(vllm_exact.TABLES["mi355x"])
+    try:
+        cfg = plugin._cfg(256, 24576, 4096)
+    finally:
+        plugin.load_table(None)
+    traffic = bench.read_traffic(cfg)
+    assert traffic is not None and traffic > bench.gemm_bytes(256, 24576, 4096)
+    assert bench.read_traffic((1, 2, 3, 4, 5, 6, 7)) is None
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stdout
 
 
 def test_custom_op_is_registered_with_fake():
