@@ -77,3 +77,29 @@ def test_op_with_packed_weights_matches_oracle(shape):
         ref = oracle.exact_linear_c(xd_np, wd_np, plugin.F, plugin.TRUNC)
         got = y.cpu().view(torch.int16).numpy().view(np.uint16)[rows]
         assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape)), M
+
+
+def test_op_row_blocks_and_input_layouts():
+    """exactmm::linear cuts M into RB-row blocks (plugin.py:60-63), each with the config of its
+    own size; rows are independent, so any blocking, a 3-D input and a transposed (strided)
+    input give the same bits as one block, and those bits equal the oracle."""
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(192, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    wbuf = plugin.pack_weight(w.to(DEV))
+    x = torch.randn(257, 1024, generator=g).to(torch.bfloat16).to(DEV)
+    full = torch.ops.exactmm.linear(x, *wbuf)
+    rb = plugin.RB
+    try:
+        plugin.RB = 100  # blocks of 100, 100 and 57 rows
+        blocked = torch.ops.exactmm.linear(x, *wbuf)
+    finally:
+        plugin.RB = rb
+    assert torch.equal(blocked, full)
+    assert torch.equal(torch.ops.exactmm.linear(x.view(1, 257, 1024), *wbuf).view(257, 192), full)
+    xt = x.t().contiguous().t()  # same values, column-major storage
+    assert xt.stride(-1) != 1 and torch.equal(torch.ops.exactmm.linear(xt, *wbuf), full)
+    rows = np.array([0, 99, 100, 256])
+    ref = oracle.exact_linear_c(oracle.digitize_c(x.float().cpu().numpy()[rows], plugin.F),
+                                oracle.digitize_c(w.float().numpy(), plugin.F), plugin.F, plugin.TRUNC)
+    got = full.cpu().view(torch.int16).numpy().view(np.uint16)[rows]
+    assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape))
