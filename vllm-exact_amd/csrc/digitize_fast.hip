@@ -2,7 +2,8 @@
 //
 // Same arithmetic as digitize.hip (kernels.py:22-39): row absmax, frexp exponent,
 // sh = F - e, q = trunc(x * 2^sh), balanced (F < 15) or offset (F == 15) digit split.
-// One workgroup of 256 lanes per row; a lane owns CPT chunks of 16 columns, issues every
+// One workgroup per row, as many lanes as the row has 16-column chunks (64 to 1024, a
+// multiple of 64); a lane owns CPT chunks of 16 columns, issues every
 // load of its chunks at once (one memory latency per row instead of one per loop trip),
 // keeps the values in registers through the absmax reduction, and writes the digits from
 // registers: 16-byte stores into the row-major planes, or into the fragment-major packed
@@ -13,7 +14,8 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kMaxThreads = 1024;
+constexpr int kMaxWaves = kMaxThreads / 64;
 
 template <int DT>
 struct In {
@@ -66,14 +68,15 @@ __device__ inline void load16(const char* row, int64_t c0, int64_t K, bool vec, 
   }
 }
 
+// Workgroup max / sum: wave reductions, then the wave results in wave order from LDS (max
+// is order-free; the int32 sum wraps like the other digitize paths).
 __device__ inline float block_max(float v, float* red) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f32(v, m));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = red[0];
-#pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, red[w]);
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
   return r;
 }
 
@@ -83,26 +86,26 @@ __device__ inline int block_sum(int v, int* red) {
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   int r = 0;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) r += red[w];
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) r += red[w];
   return r;
 }
 
 // h/l row-major planes (ldd) or packed (KT) output; PACKED selects.
 template <int DT, int CPT, bool OFFSET, bool PACKED>
-__global__ __launch_bounds__(kThreads) void digitize_fast_kernel(const void* __restrict__ x, int64_t R, int64_t K,
+__global__ __launch_bounds__(kMaxThreads) void digitize_fast_kernel(const void* __restrict__ x, int64_t R, int64_t K,
                                                                  int64_t ldx, int vec, int8_t* __restrict__ h,
                                                                  int8_t* __restrict__ l, int64_t ldd, int64_t KT,
                                                                  int32_t* __restrict__ cs, int32_t* __restrict__ sh,
                                                                  int F) {
-  __shared__ float redf[kThreads / 64];
-  __shared__ int redi[kThreads / 64];
+  __shared__ float redf[kMaxWaves];
+  __shared__ int redi[kMaxWaves];
+  const int nthr = (int)blockDim.x;
   const int64_t row = blockIdx.x;
   const int64_t nchunk = PACKED ? KT * 4 : (K + 15) / 16;
   if (PACKED && row >= R) {  // padding rows of the last tile: zero digits
     const int64_t rt = row >> 4;
     const int r16 = (int)(row & 15);
-    for (int64_t c = threadIdx.x; c < nchunk; c += kThreads) {
+    for (int64_t c = threadIdx.x; c < nchunk; c += nthr) {
       int8_t* dst = h + (rt * KT + (c >> 2)) * 2048 + ((int)(c & 3) * 16 + r16) * 16;
       *reinterpret_cast<uint4*>(dst) = uint4{0u, 0u, 0u, 0u};
       *reinterpret_cast<uint4*>(dst + 1024) = uint4{0u, 0u, 0u, 0u};
@@ -114,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void digitize_fast_kernel(const void* __r
   float v[CPT][16];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + (int64_t)i * kThreads;
+    const int64_t c = threadIdx.x + (int64_t)i * nthr;
     if (c < nchunk) {
       load16<DT>(xr, c * 16, K, vec != 0, v[i]);
     } else {
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void digitize_fast_kernel(const void* __r
   uint32_t csum = 0;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int64_t c = threadIdx.x + (int64_t)i * kThreads;
+    const int64_t c = threadIdx.x + (int64_t)i * nthr;
     if (c >= nchunk) continue;
     uint8_t hb[16], lb[16];
 #pragma unroll
@@ -182,35 +185,35 @@ __global__ __launch_bounds__(kThreads) void digitize_fast_kernel(const void* __r
 }
 
 template <int DT, bool PACKED>
-hipError_t launch_cpt(int cpt, int64_t grid_rows, const void* x, int64_t R, int64_t K, int64_t ldx, int vec,
-                      int8_t* h, int8_t* l, int64_t ldd, int64_t KT, int32_t* cs, int32_t* sh, int F,
+hipError_t launch_cpt(int cpt, int nthr, int64_t grid_rows, const void* x, int64_t R, int64_t K, int64_t ldx,
+                      int vec, int8_t* h, int8_t* l, int64_t ldd, int64_t KT, int32_t* cs, int32_t* sh, int F,
                       hipStream_t st) {
-#define VXA_DF(C)                                                                                            \
-  if (cpt == C) {                                                                                            \
-    if (F == 15)                                                                                             \
-      hipLaunchKernelGGL((digitize_fast_kernel<DT, C, true, PACKED>), dim3((unsigned)grid_rows), dim3(kThreads), \
-                         0, st, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F);                                 \
-    else                                                                                                     \
-      hipLaunchKernelGGL((digitize_fast_kernel<DT, C, false, PACKED>), dim3((unsigned)grid_rows),             \
-                         dim3(kThreads), 0, st, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F);                \
-    return hipGetLastError();                                                                                \
+#define VXA_DF(C)                                                                                           \
+  if (cpt == C) {                                                                                           \
+    if (F == 15)                                                                                            \
+      hipLaunchKernelGGL((digitize_fast_kernel<DT, C, true, PACKED>), dim3((unsigned)grid_rows), dim3(nthr), \
+                         0, st, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F);                                \
+    else                                                                                                    \
+      hipLaunchKernelGGL((digitize_fast_kernel<DT, C, false, PACKED>), dim3((unsigned)grid_rows),            \
+                         dim3(nthr), 0, st, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F);                   \
+    return hipGetLastError();                                                                               \
   }
-  VXA_DF(1) VXA_DF(2) VXA_DF(4) VXA_DF(8)
+  VXA_DF(1) VXA_DF(2)
 #undef VXA_DF
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-// Chunks of 16 columns per lane needed for K columns (1, 2, 4 or 8), or 0 when K is beyond
-// the single-pass kernel (more than 8 * 256 * 16 = 32768 columns).
-int digitize_fast_cpt(int64_t K) {
-  const int64_t per = cdiv<int64_t>(cdiv<int64_t>(K, 16), kThreads);
-  if (per <= 1) return 1;
-  if (per <= 2) return 2;
-  if (per <= 4) return 4;
-  if (per <= 8) return 8;
-  return 0;
+// Lanes per row and 16-column chunks per lane for K columns: one chunk per lane up to
+// 16384 columns (64..1024 lanes), two up to 32768; 0 chunks when K needs the multi-pass
+// kernel. The lane count is a multiple of 64 and depends only on K.
+int digitize_fast_shape(int64_t K, int* nthr) {
+  const int64_t nchunk = cdiv<int64_t>(K, 16);
+  const int cpt = nchunk <= kMaxThreads ? 1 : (nchunk <= 2 * kMaxThreads ? 2 : 0);
+  if (cpt == 0) return 0;
+  *nthr = (int)(cdiv<int64_t>(cdiv<int64_t>(nchunk, cpt), 64) * 64);
+  return cpt;
 }
 
 // Single-pass digitize into row-major planes or the packed layout. `vec` enables 16-byte
@@ -219,14 +222,15 @@ int digitize_fast_cpt(int64_t K) {
 hipError_t launch_digitize_fast(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int vec, int8_t* h,
                                 int8_t* l, int64_t ldd, bool packed, int32_t* cs, int32_t* sh, int F,
                                 hipStream_t st) {
-  const int cpt = digitize_fast_cpt(K);
+  int nthr = 0;
+  const int cpt = digitize_fast_shape(K, &nthr);
   if (cpt == 0) return hipErrorInvalidValue;
   const int64_t KT = cdiv<int64_t>(K, 64);
   const int64_t grid_rows = packed ? cdiv<int64_t>(R, 16) * 16 : R;
   if (grid_rows > 0x7FFFFFFFLL) return hipErrorInvalidConfiguration;
 #define VXA_DT(DT)                                                                                            \
-  return packed ? launch_cpt<DT, true>(cpt, grid_rows, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F, st)        \
-                : launch_cpt<DT, false>(cpt, grid_rows, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F, st);
+  return packed ? launch_cpt<DT, true>(cpt, nthr, grid_rows, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F, st)        \
+                : launch_cpt<DT, false>(cpt, nthr, grid_rows, x, R, K, ldx, vec, h, l, ldd, KT, cs, sh, F, st);
   switch (x_dtype) {
     case VXA_F32: VXA_DT(VXA_F32)
     case VXA_BF16: VXA_DT(VXA_BF16)
