@@ -50,6 +50,17 @@ __device__ inline float shfl_xor_f32(float v, int mask) {
   return shfl_f32(v, lane ^ mask);
 }
 
+// Workgroups are handed to the 8 XCDs round-robin (linear id % 8), and each XCD has its own
+// L2. This bijection gives XCD x the logical ids [x*base + min(x, rem), ...) in dispatch
+// order, so neighbouring logical tiles (which share an operand tile) run on one XCD at about
+// the same time and meet in its L2.
+__device__ inline int64_t xcd_swizzle(int64_t lin, int64_t total) {
+  constexpr int64_t kXcd = 8;
+  const int64_t xcd = lin % kXcd, j = lin / kXcd;
+  const int64_t base = total / kXcd, rem = total % kXcd;
+  return xcd * base + (xcd < rem ? xcd : rem) + j;
+}
+
 // Single-pass digitize (digitize_fast.hip) into row-major planes (h, l, ldd) or, when
 // `packed`, the fragment-major layout at h. hipErrorInvalidValue: K needs the multi-pass path.
 hipError_t launch_digitize_fast(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int vec, int8_t* h,

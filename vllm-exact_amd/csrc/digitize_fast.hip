@@ -100,7 +100,9 @@ __global__ __launch_bounds__(kMaxThreads) void digitize_fast_kernel(const void* 
   __shared__ float redf[kMaxWaves];
   __shared__ int redi[kMaxWaves];
   const int nthr = (int)blockDim.x;
-  const int64_t row = blockIdx.x;
+  // Packed digits interleave the 16 rows of a tile at 16-byte granularity: the workgroups of
+  // one tile go to one XCD (xcd_swizzle), so their partial cache lines meet in that XCD's L2.
+  const int64_t row = PACKED ? xcd_swizzle(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
   const int64_t nchunk = PACKED ? KT * 4 : (K + 15) / 16;
   if (PACKED && row >= R) {  // padding rows of the last tile: zero digits
     const int64_t rt = row >> 4;

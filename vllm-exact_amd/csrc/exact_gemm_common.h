@@ -72,17 +72,6 @@ __device__ inline void exact_store(const ExactParams& p, int split, int64_t m, i
   }
 }
 
-// Workgroups are handed to the 8 XCDs round-robin (linear id % 8), and each XCD has its own
-// L2. This bijection gives XCD x the logical ids [x*base + min(x, rem), ...) in dispatch
-// order, so neighbouring logical tiles (which share an operand tile) run on one XCD at about
-// the same time and meet in its L2.
-__device__ inline int64_t xcd_swizzle(int64_t lin, int64_t total) {
-  constexpr int64_t kXcd = 8;
-  const int64_t xcd = lin % kXcd, j = lin / kXcd;
-  const int64_t base = total / kXcd, rem = total % kXcd;
-  return xcd * base + (xcd < rem ? xcd : rem) + j;
-}
-
 __device__ inline v4i mfma_i8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 
 // Host-side launchers implemented per family (exact_gemm_sm.hip, exact_gemm_lds.hip).
