@@ -103,3 +103,27 @@ def test_op_row_blocks_and_input_layouts():
                                 oracle.digitize_c(w.float().numpy(), plugin.F), plugin.F, plugin.TRUNC)
     got = full.cpu().view(torch.int16).numpy().view(np.uint16)[rows]
     assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape))
+
+
+def test_packed_entry_points_reject_malformed_inputs():
+    """Shapes, dtypes and devices the kernels would read out of bounds are refused on the host
+    (ValueError) before any launch."""
+    x, w = xw(8, 64, 256, seed=2)
+    xp = K.digitize_packed(x.to(DEV), 14)
+    wp = K.digitize_packed(w.to(DEV), 14)
+    cfg = (16, 64, 128, 4, 1, 8, 1)
+    ok = K.exact_linear_packed(xp, wp, 256, 14, True, cfg=cfg)
+    assert ok.shape == (8, 64)
+    bad = [
+        ((xp[0], xp[1][:4], xp[2]), wp),                          # cx shorter than M
+        (xp, (wp[0], wp[1], wp[2].to(torch.int64))),              # sw not int32
+        ((xp[0].view(torch.uint8), xp[1], xp[2]), wp),            # packed digits not int8
+        (xp, (wp[0][:2], wp[1], wp[2])),                          # packed rows do not match N
+    ]
+    for a, b in bad:
+        with pytest.raises(ValueError):
+            K.exact_linear_packed(a, b, 256, 14, True, cfg=cfg)
+    with pytest.raises(ValueError):
+        K.exact_linear_packed(xp, wp, 320, 14, True, cfg=cfg)   # K disagrees with the packed shape
+    with pytest.raises(ValueError):
+        K.digitize_packed(x.to(DEV), 14, out=(xp[0], xp[1][:3], xp[2]))

@@ -107,6 +107,14 @@ def exact_linear_torch(xd, wd, F, trunc=False):
     return (tot.double() * two_e).float()
 
 
+def _check_sums(name, cs, sh, rows):
+    """The per-row digit sums and scale exponents the kernels read: int32, contiguous, `rows` each."""
+    if cs.dtype != torch.int32 or sh.dtype != torch.int32 or cs.numel() != rows or sh.numel() != rows:
+        raise ValueError(f"{name}: cs/sh must be int32 tensors of {rows} elements")
+    if not (cs.is_contiguous() and sh.is_contiguous()):
+        raise ValueError(f"{name}: cs/sh must be contiguous")
+
+
 # ======================= packed (fragment-major) digits =======================
 # A [R, K] digit matrix packs into int8 [cdiv(R,16), cdiv(K,64), 2, 1024]: block (rt, kt) holds
 # the h then l fragment of rows 16rt..16rt+15 and columns 64kt..64kt+63 in the operand order of
@@ -147,6 +155,9 @@ def digitize_packed(x, F, out=None):
     packed, cs, sh = out
     if packed.shape != packed_shape(R, K) or not packed.is_contiguous() or packed.dtype != torch.int8:
         raise ValueError("digitize_packed: packed must be a contiguous int8 tensor of packed_shape(R, K)")
+    _check_sums("digitize_packed", cs, sh, R)
+    if any(t.device != dev for t in out):
+        raise ValueError("digitize_packed: outputs must be on the input's device")
     with torch.cuda.device(dev):
         _nx.check(_nx.lib().vxa_digitize_packed(x.data_ptr(), _nx.dtype_enum(x.dtype), R, K, x.stride(0),
                                                 packed.data_ptr(), cs.data_ptr(), sh.data_ptr(), F,
@@ -161,11 +172,17 @@ def exact_linear_packed(xp, wp, K, F, trunc=False, out=None, cfg=None):
     pw, cw, sw = wp
     _require_gpu(px, "exact_linear_packed")
     M, N = sx.numel(), sw.numel()
+    if px.dtype != torch.int8 or pw.dtype != torch.int8:
+        raise ValueError("exact_linear_packed: packed digits must be int8")
     if px.shape != packed_shape(M, K) or pw.shape != packed_shape(N, K):
         raise ValueError("exact_linear_packed: packed shapes do not match (M, K) and (N, K)")
     if not (px.is_contiguous() and pw.is_contiguous()):
         raise ValueError("exact_linear_packed: packed digits must be contiguous")
+    _check_sums("exact_linear_packed (x)", cx, sx, M)
+    _check_sums("exact_linear_packed (w)", cw, sw, N)
     dev = px.device
+    if any(t.device != dev for t in (*xp, *wp)):
+        raise ValueError("exact_linear_packed: all digit tensors must be on one device")
     if out is None:
         out = torch.empty((M, N), device=dev, dtype=torch.float32)
     if out.shape != (M, N) or out.stride(1) != 1 or out.device != dev:
@@ -184,12 +201,14 @@ def exact_linear_packed(xp, wp, K, F, trunc=False, out=None, cfg=None):
     return out
 
 
-# gfx950 kernel shapes, as cfg tuples (BM, BN, BK, warps, stages, GM). Two families:
+# gfx950 kernel shapes, as cfg tuples (BM, BN, BK, warps, stages, GM). Three families:
 # * small-M register-streaming kernel: BM = 16*MT rows, BN = 16*NT columns per workgroup,
 #   `warps` waves splitting K, `stages` = K steps whose loads are issued together;
 # * LDS-ring kernel (BM, BN >= 64, 4 waves, stages >= 2): BM x BN tile, `stages`-deep ring
-#   of direct-to-LDS loads.
-# BK only rounds split-K chunks; GM is accepted for the reference's format.
+#   of direct-to-LDS loads;
+# * x-through-LDS kernel (BK = 64, packed digits): BM x BN tile, `warps` = 4 or 8 waves,
+#   `stages` = weight register sets in flight per wave.
+# BK otherwise only rounds split-K chunks; GM is accepted for the reference's format.
 SMALL_SHAPES = [(1, 1, 1, 4), (1, 1, 1, 8), (1, 1, 1, 16), (1, 1, 2, 4), (1, 1, 2, 8), (1, 1, 2, 16), (1, 1, 4, 4),
                 (1, 1, 4, 8), (1, 1, 4, 16), (1, 2, 1, 4), (1, 2, 1, 8), (1, 2, 1, 16), (1, 2, 2, 4), (1, 2, 2, 8),
                 (1, 2, 2, 16), (1, 2, 4, 4), (1, 2, 4, 8), (1, 4, 1, 4), (1, 4, 1, 8), (1, 4, 1, 16), (1, 4, 2, 4),
