@@ -12,7 +12,8 @@ sit in HBM before timing starts. `value` is the sweep's algorithmic bytes
 (2NK + 2MK + 2MN + 8N per linear) over the step time.
 
 Also reported, from the same run:
-* per-op times with GB/s, TOPS and roofline fractions, and the hipBLASLt bf16 time;
+* per-op times with GB/s, TOPS and roofline fractions, the hipBLASLt bf16 time and, for
+  M > 16, the vendor int8 GEMM (torch._int_mm, one dot) on the same shape;
 * `roofline` of the dominant kernel (the GEMM launch with the largest share of the step),
   timed alone with HIP events on its own stream;
 * split-bf16 paged decode attention at H=32/KV=8/D=128/BS=16 for 64x8K, 16x16K, 256x1K (TB/s);
@@ -294,10 +295,23 @@ def main():
         wbs = [wb.clone() for _ in range(min(rot, rotations_for(2 * N * Kd)))]
         t_bf16 = time_graph(lambda r: torch.matmul(xs[(M, Kd)], wbs[r].T), len(wbs))
         del wbs
+        # the vendor int8 GEMM (torch._int_mm, one int8 dot, int32 out) on the same shape, for
+        # scale: the exact path runs three such dots
+        t_i8 = None
+        if M > 16:
+            a8 = torch.randint(-128, 128, (M, Kd), dtype=torch.int8, device=dev, generator=gen)
+            b8 = [torch.randint(-128, 128, (N, Kd), dtype=torch.int8, device=dev, generator=gen)
+                  for _ in range(min(rot, rotations_for(N * Kd)))]
+            try:
+                t_i8 = round(time_graph(lambda r: torch._int_mm(a8, b8[r].T), len(b8)), 2)
+            except RuntimeError:
+                t_i8 = None
+            del a8, b8
         b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
         t_roof = max(b / (HBM_PEAK_GBS * 1e9), o / (INT8_PEAK_TOPS * 1e12)) * 1e6
         rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
-                   bf16_hipblaslt_us=round(t_bf16, 2), gemm_GBps=round(b / t_gemm / 1e3, 1),
+                   bf16_hipblaslt_us=round(t_bf16, 2), int8_1dot_vendor_us=t_i8,
+                   gemm_GBps=round(b / t_gemm / 1e3, 1),
                    gemm_TOPS=round(o / t_gemm / 1e6, 1), hbm_frac=round(b / t_gemm / 1e3 / HBM_PEAK_GBS, 3),
                    mfma_frac=round(o / t_gemm / 1e6 / INT8_PEAK_TOPS, 3), roofline_frac=round(t_roof / t_gemm, 3),
                    bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma",
