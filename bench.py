@@ -242,10 +242,6 @@ def main():
     def op_call(M, name, Kd, r):
         return torch.ops.exactmm.linear(xs[(M, Kd)], *weights[name][r])
 
-    def gemm_call(xd, name, Kd, r, cfg):
-        wp, _, cw, sw = weights[name][r]
-        return K.exact_linear_packed(xd, (wp, cw, sw), Kd, F, TRUNC, cfg=cfg)
-
     # ---------------------------------------------------------------- the step graph
     def step_calls(r):
         # each op uses copy (r + op index) % rot, so consecutive uses of a shape's weights differ
@@ -285,48 +281,59 @@ def main():
     del graphs
 
     # ---------------------------------------------------------------- per-op detail
-    per_op = []
-    for M, name, N, Kd in ops:
-        cfg = plugin._cfg(M, N, Kd)
-        xd = K.digitize_packed(xs[(M, Kd)], F)
-        t_op = time_graph(lambda r: op_call(M, name, Kd, r), rot)
-        t_gemm = time_graph(lambda r: gemm_call(xd, name, Kd, r, cfg), rot)
-        wb = weights[name + ".bf16"]
-        wbs = [wb.clone() for _ in range(min(rot, rotations_for(2 * N * Kd)))]
-        t_bf16 = time_graph(lambda r: torch.matmul(xs[(M, Kd)], wbs[r].T), len(wbs))
-        del wbs
+    # Each shape is timed on enough weight copies that one rotation streams >= 768 MB, past
+    # the 256 MB MALL (three copies of a small shape would stay in it).
+    per_op = {}
+    for name, N, Kd in SHAPES:
+        nrot = max(rot, rotations_for(2 * N * Kd))
+        wc = weights[name] + [tuple(t.clone() for t in weights[name][0]) for _ in range(nrot - rot)]
+        wbs = [weights[name + ".bf16"].clone() for _ in range(rotations_for(2 * N * Kd))]
         # the vendor int8 GEMM (torch._int_mm, one int8 dot, int32 out) on the same shape, for
         # scale: the exact path runs three such dots
-        t_i8 = None
-        if M > 16:
-            a8 = torch.randint(-128, 128, (M, Kd), dtype=torch.int8, device=dev, generator=gen)
-            b8 = [torch.randint(-128, 128, (N, Kd), dtype=torch.int8, device=dev, generator=gen)
-                  for _ in range(min(rot, rotations_for(N * Kd)))]
-            try:
-                t_i8 = round(time_graph(lambda r: torch._int_mm(a8, b8[r].T), len(b8)), 2)
-            except RuntimeError:
-                t_i8 = None
-            del a8, b8
-        b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
-        t_roof = max(b / (HBM_PEAK_GBS * 1e9), o / (INT8_PEAK_TOPS * 1e12)) * 1e6
-        rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
-                   bf16_hipblaslt_us=round(t_bf16, 2), int8_1dot_vendor_us=t_i8,
-                   gemm_GBps=round(b / t_gemm / 1e3, 1),
-                   gemm_TOPS=round(o / t_gemm / 1e6, 1), hbm_frac=round(b / t_gemm / 1e3 / HBM_PEAK_GBS, 3),
-                   mfma_frac=round(o / t_gemm / 1e6 / INT8_PEAK_TOPS, 3), roofline_frac=round(t_roof / t_gemm, 3),
-                   bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma",
-                   vs_bf16=round(t_op / t_bf16, 2))
-        per_op.append(rec)
-        log(json.dumps(rec))
+        b8 = [torch.randint(-128, 128, (N, Kd), dtype=torch.int8, device=dev, generator=gen)
+              for _ in range(rotations_for(N * Kd))]
+        for M in MS:
+            cfg = plugin._cfg(M, N, Kd)
+            x = xs[(M, Kd)]
+            xd = K.digitize_packed(x, F)
+            t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
+            t_gemm = time_graph(lambda r: K.exact_linear_packed(xd, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, TRUNC,
+                                                                cfg=cfg), nrot)
+            t_bf16 = time_graph(lambda r: torch.matmul(x, wbs[r].T), len(wbs))
+            t_i8 = None
+            if M > 16:
+                a8 = torch.randint(-128, 128, (M, Kd), dtype=torch.int8, device=dev, generator=gen)
+                try:
+                    t_i8 = round(time_graph(lambda r: torch._int_mm(a8, b8[r].T), len(b8)), 2)
+                except RuntimeError:
+                    t_i8 = None
+            b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
+            t_roof = max(b / (HBM_PEAK_GBS * 1e9), o / (INT8_PEAK_TOPS * 1e12)) * 1e6
+            rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
+                       bf16_hipblaslt_us=round(t_bf16, 2), int8_1dot_vendor_us=t_i8,
+                       gemm_GBps=round(b / t_gemm / 1e3, 1),
+                       gemm_TOPS=round(o / t_gemm / 1e6, 1), hbm_frac=round(b / t_gemm / 1e3 / HBM_PEAK_GBS, 3),
+                       mfma_frac=round(o / t_gemm / 1e6 / INT8_PEAK_TOPS, 3), roofline_frac=round(t_roof / t_gemm, 3),
+                       bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma",
+                       vs_bf16=round(t_op / t_bf16, 2), weight_copies=nrot)
+            per_op[(M, name)] = rec
+            log(json.dumps(rec))
+        del wc, wbs, b8
+        torch.cuda.empty_cache()
+    per_op = [per_op[(M, name)] for M, name, _, _ in ops]
 
     # dominant kernel: the GEMM with the largest share of the step, timed alone on its stream
     dom = max(per_op, key=lambda r: r["gemm_us"])
     M, N, Kd, name = dom["M"], dom["N"], dom["K"], dom["op"]
     cfg = tuple(dom["cfg"])
     xd = K.digitize_packed(xs[(M, Kd)], F)
+    nrot = max(rot, rotations_for(2 * N * Kd))
+    wc = weights[name] + [tuple(t.clone() for t in weights[name][0]) for _ in range(nrot - rot)]
     kstream = torch.cuda.Stream()
     with torch.cuda.stream(kstream):
-        t_kernel = time_graph(lambda r: gemm_call(xd, name, Kd, r, cfg), rot, calls_per_replay=20, replays=30)
+        t_kernel = time_graph(lambda r: K.exact_linear_packed(xd, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, TRUNC,
+                                                              cfg=cfg), nrot, calls_per_replay=20, replays=30)
+    del wc
     b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
     if dom["bound"] == "hbm":
         roof = dict(bound="hbm", achieved=round(b / t_kernel / 1e3, 1), peak=HBM_PEAK_GBS, unit="GB/s",

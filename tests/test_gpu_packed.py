@@ -23,7 +23,7 @@ DEV = "cuda"
 PACKED_CFGS = ((16, 16, 128, 16, 4, 8), (16, 32, 128, 8, 2, 8), (16, 64, 128, 4, 1, 8), (32, 64, 128, 8, 1, 8),
                (64, 32, 128, 4, 2, 8), (64, 64, 128, 4, 1, 8), (64, 64, 128, 4, 8, 8), (128, 64, 128, 4, 6, 8),
                (64, 128, 128, 4, 4, 8), (128, 128, 128, 4, 4, 8), (128, 128, 128, 4, 2, 8)) + tuple(
-    (bm, 4 * wn, 64, nw, r, 8) for bm, wn, r, nw in K.XW_SHAPES)  # BK = 64: x through LDS, weights in registers
+    (bm, bn, 64, nw, r, 8) for bm, bn, r, nw in K.XW_SHAPES)  # BK = 64: x through LDS, weights in registers
 
 
 @pytest.mark.parametrize("R,Kd", [(16, 4096), (37, 1000), (5, 64), (300, 12288), (3, 40000)])

@@ -48,7 +48,7 @@ def test_shipped_table_is_well_formed():
     plugin.load_table(None)
     # every entry names an instantiated kernel: x-through-LDS tiles (BK = 64) exactly, the
     # other families through the plan's nearest-instantiation rule
-    xw = {(bm, 4 * wn, r, nw) for bm, wn, r, nw in K.XW_SHAPES}
+    xw = {(bm, bn, r, nw) for bm, bn, r, nw in K.XW_SHAPES}
     for row in raw.values():
         for cfg in row.values():
             if cfg[2] == 64:

@@ -58,7 +58,7 @@ int lds_stages(int bm, int bn, int want) {
 }
 
 // cfg tuple (BM, BN, BK, warps, stages, GM[, SK[, mma]]) -> kernel family and shape:
-//   BK == 64, warps 4 or 8: on packed operands, the x-through-LDS kernel with tile BM x BN,
+//   BK == 64, warps 3, 4, 6 or 8: on packed operands, the x-through-LDS kernel with tile BM x BN,
 //     R = stages weight register sets and `warps` waves when instantiated (exact_xw_supported); otherwise, and
 //     on row-major digits, the LDS-ring kernel below with BM and BN clamped to 64..128;
 //   BM >= 64, BN >= 64, warps == 4, stages >= 2: LDS-ring kernel with tile
@@ -75,7 +75,7 @@ int make_plan(int64_t K, const int32_t* cfg, int cfg_len, ExactPlan* out) {
   const int32_t SKr = cfg_len > 6 ? cfg[6] : 1;
   if (BM <= 0 || BN <= 0 || BK <= 0 || warps <= 0 || stages <= 0 || SKr <= 0) return VXA_ERR_ARG;
   ExactPlan p = {};
-  if (BK == 64 && (warps == 4 || warps == 8)) {
+  if (BK == 64 && (warps == 3 || warps == 4 || warps == 6 || warps == 8)) {
     p.family = kFamilyXw;
     p.bm = BM;
     p.bn = BN;

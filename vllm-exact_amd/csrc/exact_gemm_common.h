@@ -43,7 +43,7 @@ struct ExactPlan {
   // C 64-wide K steps whose loads are issued together
   int mt, nt, nwk, chunk;
   // LDS pipeline kernel: BM x BN workgroup tile, S ring stages; x-through-LDS kernel:
-  // BM x BN workgroup tile, `stages` = R weight register sets, `nwk` = 4 or 8 waves
+  // BM x BN workgroup tile, `stages` = R weight register sets, `nwk` = 3, 4, 6 or 8 waves
   int bm, bn, stages;
   int64_t kch;
   int32_t sk;

@@ -1,11 +1,12 @@
 // Large-M exact GEMM on packed digits: the x tile through an LDS ring, the weight fragments
 // straight into registers.
 //
-// Workgroup tile BM x (4 * WN): 4 waves side by side along N, each computing all BM rows of
-// its WN columns. The x fragments of a K step (BM/16 tiles x 2 digit planes, 1 KiB each in
-// MFMA lane order) are shared by the 4 waves, so they go through a ring of S = R + 1 LDS
-// stages filled by global_load_lds_dwordx4 (gfx950 direct-to-LDS loads, a quarter of the
-// fragments per wave). The weight fragments of a wave are its own: each is one contiguous
+// Workgroup tile BM x (NWN * WN): NWN waves side by side along N, each computing all BM rows
+// of its WN columns (times WMS waves along M, each on BM / WMS rows). The x fragments of a K
+// step (BM/16 tiles x 2 digit planes, 1 KiB each in MFMA lane order) are shared by the waves,
+// so they go through a ring of S = R + 1 LDS stages filled by global_load_lds_dwordx4 (gfx950
+// direct-to-LDS loads, split over the waves; when the count does not divide evenly, some
+// waves copy one fragment a second time, the same bytes to the same place). The weight fragments of a wave are its own: each is one contiguous
 // 1 KiB global_load_dwordx4 per wave straight into a ring of R register sets, so the weight
 // stream (the HBM-bound operand) keeps R steps in flight per wave without using LDS.
 //
@@ -31,26 +32,26 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int BM, int WN, int R, int WMS, bool TRUNC>
-__global__ __launch_bounds__(256 * WMS) void exact_xw_kernel(ExactParams p) {
-  constexpr int NWAVE = 4 * WMS;  // waves: 4 along N times WMS along M
-  constexpr int TMA = BM / 16;    // 16-row tiles of the x tile
-  constexpr int TM = TMA / WMS;   // ... of one wave
-  constexpr int TN = WN / 16;     // 16-column tiles of one wave
-  constexpr int BN = 4 * WN;      // workgroup tile width
-  constexpr int S = R + 1;        // x ring stages
-  constexpr int NFX = 2 * TMA;    // x fragments per stage (h and l planes)
-  constexpr int LX = NFX / NWAVE; // x fragments each wave loads per stage
-  constexpr int LW = 2 * TN;      // weight fragments each wave loads per step
+template <int BM, int NWN, int WN, int R, int WMS, bool TRUNC>
+__global__ __launch_bounds__(64 * NWN * WMS) void exact_xw_kernel(ExactParams p) {
+  constexpr int NWAVE = NWN * WMS;  // waves: NWN along N times WMS along M
+  constexpr int TMA = BM / 16;      // 16-row tiles of the x tile
+  constexpr int TM = TMA / WMS;     // ... of one wave
+  constexpr int TN = WN / 16;       // 16-column tiles of one wave
+  constexpr int BN = NWN * WN;      // workgroup tile width
+  constexpr int S = R + 1;          // x ring stages
+  constexpr int NFX = 2 * TMA;      // x fragments per stage (h and l planes)
+  constexpr int LX = (NFX + NWAVE - 1) / NWAVE;  // x fragments each wave copies per stage
+  constexpr int LW = 2 * TN;        // weight fragments each wave loads per step
   constexpr int kWait = (R - 1) * (LX + LW);
-  static_assert(TMA % WMS == 0 && NFX % NWAVE == 0, "x fragments split evenly over the waves");
+  static_assert(TMA % WMS == 0, "row tiles split evenly over the waves along M");
   static_assert(kWait <= 63, "vmcnt limit");
   __shared__ __attribute__((aligned(1024))) int8_t ring[S * NFX * 1024];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wn = wave & 3;   // column block of this wave
-  const int wm = wave >> 2;  // row block of this wave (WMS > 1)
+  const int wn = wave % NWN;  // column block of this wave
+  const int wm = wave / NWN;  // row block of this wave (WMS > 1)
 
   // Logical tile order: M tiles fastest, then N tiles, then K splits; the workgroups that
   // share one weight tile are neighbours and, through xcd_swizzle, on one XCD.
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256 * WMS) void exact_xw_kernel(ExactParams p) {
   int xdst[LX];
 #pragma unroll
   for (int i = 0; i < LX; ++i) {
-    const int f = wave + NWAVE * i;  // fragment f: plane f / TMA, tile f % TMA
+    const int f = (wave + NWAVE * i) % NFX;  // fragment f: plane f / TMA, tile f % TMA
     const int64_t tile = min(bm * TMA + f % TMA, cdiv<int64_t>(p.M, 16) - 1);
     xsrc[i] = p.xh + (tile * p.KT + kt0) * 2048 + (f / TMA) * 1024 + lane * 16;
     xdst[i] = f * 1024;
@@ -204,29 +205,32 @@ __global__ __launch_bounds__(256 * WMS) void exact_xw_kernel(ExactParams p) {
       }
 }
 
-template <int BM, int WN, int R, int WMS, bool TRUNC>
+template <int BM, int NWN, int WN, int R, int WMS, bool TRUNC>
 hipError_t launch(const ExactParams& ep, hipStream_t st) {
-  const int64_t blocks = cdiv<int64_t>(ep.M, BM) * cdiv<int64_t>(ep.N, 4 * WN);
+  const int64_t blocks = cdiv<int64_t>(ep.M, BM) * cdiv<int64_t>(ep.N, NWN * WN);
   if (blocks > 0x7FFFFFFFLL || ep.sk > 65535) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((exact_xw_kernel<BM, WN, R, WMS, TRUNC>), dim3((unsigned)blocks, (unsigned)ep.sk),
-                     dim3(256 * WMS), 0, st, ep);
+  hipLaunchKernelGGL((exact_xw_kernel<BM, NWN, WN, R, WMS, TRUNC>), dim3((unsigned)blocks, (unsigned)ep.sk),
+                     dim3(64 * NWN * WMS), 0, st, ep);
   return hipGetLastError();
 }
 
-// Instantiated (BM, WN, R, WMS); the 4-dot (F = 15) variants only where three accumulator
-// sets fit. WMS = 2 runs 8 waves (two per SIMD), each on half of the BM rows.
+// Instantiated (BM, NWN, WN, R, WMS); the 4-dot (F = 15) variants only where three
+// accumulator sets fit. WMS = 2 runs two waves per SIMD, each on half of the BM rows. The
+// 96-column tiles (NWN = 3 or 6) put a 24576-column product on 256 workgroups.
 #define VXA_XW_TABLE(X)                                                                                   \
-  X(32, 32, 4, 1, 1) X(32, 64, 4, 1, 1) X(64, 16, 4, 1, 1) X(64, 32, 4, 1, 1) X(64, 48, 4, 1, 1)          \
-  X(64, 64, 3, 1, 1) X(64, 64, 4, 1, 0) X(128, 16, 4, 1, 1) X(128, 32, 3, 1, 1) X(128, 32, 4, 1, 0)       \
-  X(128, 48, 3, 1, 0) X(128, 48, 4, 1, 0) X(64, 32, 4, 2, 1) X(64, 48, 4, 2, 1) X(64, 64, 4, 2, 0)        \
-  X(128, 32, 4, 2, 1) X(128, 48, 3, 2, 0) X(128, 48, 4, 2, 0) X(128, 64, 2, 2, 0)
+  X(32, 4, 32, 4, 1, 1) X(32, 4, 64, 4, 1, 1) X(64, 4, 16, 4, 1, 1) X(64, 4, 32, 4, 1, 1)                 \
+  X(64, 4, 48, 4, 1, 1) X(64, 4, 64, 3, 1, 1) X(64, 4, 64, 4, 1, 0) X(128, 4, 16, 4, 1, 1)                \
+  X(128, 4, 32, 3, 1, 1) X(128, 4, 32, 4, 1, 0) X(128, 4, 48, 3, 1, 0) X(128, 4, 48, 4, 1, 0)             \
+  X(64, 4, 32, 4, 2, 1) X(64, 4, 48, 4, 2, 1) X(64, 4, 64, 4, 2, 0) X(128, 4, 32, 4, 2, 1)                \
+  X(128, 4, 48, 3, 2, 0) X(128, 4, 48, 4, 2, 0) X(128, 4, 64, 2, 2, 0) X(64, 6, 16, 4, 1, 1)              \
+  X(64, 6, 16, 6, 1, 1) X(64, 6, 16, 8, 1, 1) X(64, 3, 32, 4, 1, 1) X(64, 3, 32, 6, 1, 1)
 
 template <bool TRUNC>
 hipError_t dispatch(const ExactPlan& pl, const ExactParams& ep, hipStream_t st) {
-#define VXA_XW(BM_, WN_, R_, WMS_, FOUR_)                                                  \
+#define VXA_XW(BM_, NWN_, WN_, R_, WMS_, FOUR_)                                             \
   if constexpr (TRUNC || FOUR_) {                                                           \
-    if (pl.bm == BM_ && pl.bn == 4 * WN_ && pl.stages == R_ && pl.nwk == 4 * WMS_)          \
-      return launch<BM_, WN_, R_, WMS_, TRUNC>(ep, st);                                     \
+    if (pl.bm == BM_ && pl.bn == NWN_ * WN_ && pl.stages == R_ && pl.nwk == NWN_ * WMS_)    \
+      return launch<BM_, NWN_, WN_, R_, WMS_, TRUNC>(ep, st);                               \
   }
   VXA_XW_TABLE(VXA_XW)
 #undef VXA_XW
@@ -236,8 +240,8 @@ hipError_t dispatch(const ExactPlan& pl, const ExactParams& ep, hipStream_t st) 
 }  // namespace
 
 bool exact_xw_supported(int bm, int bn, int r, int waves, bool trunc) {
-#define VXA_XW_HAS(BM_, WN_, R_, WMS_, FOUR_) \
-  if (bm == BM_ && bn == 4 * WN_ && r == R_ && waves == 4 * WMS_ && (trunc || FOUR_)) return true;
+#define VXA_XW_HAS(BM_, NWN_, WN_, R_, WMS_, FOUR_) \
+  if (bm == BM_ && bn == NWN_ * WN_ && r == R_ && waves == NWN_ * WMS_ && (trunc || FOUR_)) return true;
   VXA_XW_TABLE(VXA_XW_HAS)
 #undef VXA_XW_HAS
   return false;

@@ -217,13 +217,14 @@ SMALL_SHAPES = [(1, 1, 1, 4), (1, 1, 1, 8), (1, 1, 1, 16), (1, 1, 2, 4), (1, 1, 
                 (4, 1, 1, 8), (4, 1, 2, 4), (4, 1, 2, 8), (4, 2, 1, 4), (4, 2, 1, 8), (4, 4, 1, 4)]  # (MT, NT, C, NWK)
 LDS_SHAPES = [(64, 64, 2), (64, 64, 4), (64, 64, 8), (128, 64, 2), (128, 64, 4), (128, 64, 6), (64, 128, 2),
               (64, 128, 4), (64, 128, 6), (128, 128, 2), (128, 128, 3), (128, 128, 4)]  # (BM, BN, stages)
-XW_SHAPES = [(32, 32, 4, 4), (32, 64, 4, 4), (64, 16, 4, 4), (64, 32, 4, 4), (64, 48, 4, 4), (64, 64, 3, 4),
-             (64, 64, 4, 4), (128, 16, 4, 4), (128, 32, 3, 4), (128, 32, 4, 4), (128, 48, 3, 4), (128, 48, 4, 4),
-             (64, 32, 4, 8), (64, 48, 4, 8), (64, 64, 4, 8), (128, 32, 4, 8), (128, 48, 3, 8), (128, 48, 4, 8),
-             (128, 64, 2, 8)]  # (BM, columns per wave, weight sets, waves); BK = 64
+XW_SHAPES = [(32, 128, 4, 4), (32, 256, 4, 4), (64, 64, 4, 4), (64, 128, 4, 4), (64, 192, 4, 4), (64, 256, 3, 4),
+             (64, 256, 4, 4), (128, 64, 4, 4), (128, 128, 3, 4), (128, 128, 4, 4), (128, 192, 3, 4),
+             (128, 192, 4, 4), (64, 128, 4, 8), (64, 192, 4, 8), (64, 256, 4, 8), (128, 128, 4, 8),
+             (128, 192, 3, 8), (128, 192, 4, 8), (128, 256, 2, 8), (64, 96, 4, 6), (64, 96, 6, 6), (64, 96, 8, 6),
+             (64, 96, 4, 3), (64, 96, 6, 3)]  # (BM, BN, weight sets, waves); BK = 64
 EXACT_CFGS = ([(16 * mt, 16 * nt, 128, nwk, c, 8) for mt, nt, c, nwk in SMALL_SHAPES]
               + [(bm, bn, 128, 4, st, 8) for bm, bn, st in LDS_SHAPES]
-              + [(bm, 4 * wn, 64, nw, r, 8) for bm, wn, r, nw in XW_SHAPES])
+              + [(bm, bn, 64, nw, r, 8) for bm, bn, r, nw in XW_SHAPES])
 AUTOTUNE_SPLITS = (1, 2, 4)
 _CFG_CACHE = {}
 
