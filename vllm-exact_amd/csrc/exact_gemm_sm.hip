@@ -44,8 +44,12 @@ __global__ __launch_bounds__(64 * NWK) void exact_sm_kernel(ExactParams p) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     if constexpr (PACKED) {
+      // Lanes of rows past M (zero padding of the last tile, or a clamped tile) read the
+      // fragment's first 16 bytes instead, which row 0's lanes fetch anyway: at M = 1 that
+      // halves the x bytes moved per fragment. Their results are never stored.
       const int64_t tile = min(bm * MT + mt, cdiv<int64_t>(p.M, 16) - 1);
-      xhp[mt] = p.xh + (tile * p.KT + (kb >> 6)) * 2048 + lane * 16;
+      const bool row_ok = m0 + mt * 16 + r16 < p.M;
+      xhp[mt] = p.xh + (tile * p.KT + (kb >> 6)) * 2048 + (row_ok ? lane * 16 : 0);
       xlp[mt] = xhp[mt] + 1024;
     } else {
       const int64_t m = min(m0 + mt * 16 + r16, p.M - 1);
