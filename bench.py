@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-attention] [--no-decode-step] [--no-cpu]
     python bench.py --profile-kernel [--steps K]   (launches for rocprofv3 counter runs)
+    python bench.py --profile-counters             (every sweep GEMM and attention shape, for counter runs)
 
 Step: one pass of the decode-shaped exact linear sweep (the BASELINE workload for this
 metric): QKV 4096->6144, O 4096->4096, gate_up 4096->24576 and down 12288->4096 at
@@ -135,6 +136,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
                     help="exact_int8 tuning table to use")
+    ap.add_argument("--profile-counters", action="store_true",
+                    help="only launch every sweep GEMM (table cfg, weights rotated past the MALL) and the three "
+                         "decode-attention shapes, 5 times each, then a 1 GiB copy: the program rocprofv3 --pmc "
+                         "passes (MFMA utilisation, FETCH_SIZE, WRITE_SIZE) run; one JSON line per launch group")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant GEMM (M=256 gate_up, table cfg) and a 1 GiB copy, --steps times "
                          "each: the program rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs to measure HBM traffic")
@@ -196,6 +201,70 @@ def profile_kernel(args):
                       "copy_bytes": src.numel() * 2, "algorithmic_bytes": gemm_bytes(M, N, Kd)}), flush=True)
 
 
+def profile_counters(args):
+    """Launch each sweep GEMM and each decode-attention shape a few times, in a fixed order, for
+    rocprofv3 counter passes; print one JSON line per group (what ran, how many launches, its
+    algorithmic bytes and ops) so the counter rows can be matched to the ops."""
+    import torch
+
+    from vllm_exact import _native
+    from vllm_exact import kernels as K
+    from vllm_exact import paged_attn as P
+    from vllm_exact import plugin
+    from vllm_exact.graph_timing import rotations_for
+
+    _native.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    plugin.load_table(args.table)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    n = 5
+    for name, N, Kd in SHAPES:
+        w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        w0 = plugin.pack_weight(w)
+        wc = [w0] + [tuple(t.clone() for t in w0) for _ in range(rotations_for(2 * N * Kd) - 1)]
+        for M in MS:
+            cfg = plugin._cfg(M, N, Kd)
+            x = torch.randn(M, Kd, device=dev, generator=gen).to(torch.bfloat16)
+            xd = K.digitize_packed(x, F)
+            out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+            for i in range(n):
+                r = wc[i % len(wc)]
+                K.exact_linear_packed(xd, (r[0], r[2], r[3]), Kd, F, TRUNC, out=out, cfg=cfg)
+            torch.cuda.synchronize()
+            print(json.dumps({"group": "gemm", "op": name, "M": M, "N": N, "K": Kd, "cfg": list(cfg), "launches": n,
+                              "algorithmic_bytes": gemm_bytes(M, N, Kd), "algorithmic_ops": gemm_ops(M, N, Kd)}),
+                  flush=True)
+        del wc, w0
+        torch.cuda.empty_cache()
+    H, KV, D, BS = 32, 8, 128, 16
+    P.MAX_LEN = 16384
+    for B, L in ATTN_CASES:
+        nbp = L // BS
+        kv = torch.randn(B * nbp, KV, BS, 2 * D, device=dev, generator=gen, dtype=torch.bfloat16)
+        bt = torch.randperm(B * nbp, device=dev, generator=gen).view(B, nbp).to(torch.int32)
+        q = torch.randn(B, H, D, device=dev, generator=gen, dtype=torch.bfloat16)
+        sl = torch.full((B,), L, device=dev, dtype=torch.int32)
+        kc, vc = kv.transpose(1, 2).split(D, dim=-1)
+        out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            P.paged_decode(q, kc, vc, bt, sl, D ** -0.5, out, B, L)
+        torch.cuda.synchronize()
+        print(json.dumps({"group": "attention", "B": B, "L": L, "launches": 3, "kv_bytes": B * L * KV * D * 2 * 2}),
+              flush=True)
+        del kv, kc, vc
+        torch.cuda.empty_cache()
+    src = torch.randn(1 << 29, device=dev, generator=gen).to(torch.bfloat16)  # 1 GiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"group": "copy", "launches": 3, "bytes": src.numel() * 2}), flush=True)
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -208,6 +277,9 @@ def main():
         sys.exit(2)
     if args.profile_kernel:
         profile_kernel(args)
+        return
+    if args.profile_counters:
+        profile_counters(args)
         return
     import numpy as np
     import torch
