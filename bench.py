@@ -14,7 +14,9 @@ sit in HBM before timing starts. `value` is the sweep's algorithmic bytes
 
 Also reported, from the same run:
 * per-op times with GB/s, TOPS and roofline fractions, the hipBLASLt bf16 time and, for
-  M > 16, the vendor int8 GEMM (torch._int_mm, one dot) on the same shape;
+  M > 16, the vendor int8 GEMM (torch._int_mm, one dot) on the same shape; `gemm_us` is the
+  kernel the op runs without the digitize launch (at 1-4 rows the one-launch digitize + GEMM
+  kernel, `one_launch`);
 * `roofline` of the dominant kernel (the GEMM launch with the largest share of the step),
   timed alone with HIP events on its own stream;
 * split-bf16 paged decode attention at H=32/KV=8/D=128/BS=16 for 64x8K, 16x16K, 256x1K (TB/s);
@@ -369,8 +371,20 @@ def main():
             x = xs[(M, Kd)]
             xd = K.digitize_packed(x, F)
             t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
-            t_gemm = time_graph(lambda r: K.exact_linear_packed(xd, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, TRUNC,
-                                                                cfg=cfg), nrot)
+            # the GEMM kernel the op runs: at 1-4 rows the one-launch digitize + GEMM kernel
+            # (x read as bf16), otherwise the GEMM on digits digitized beforehand
+            one_launch = M <= K.FUSED_MAX_ROWS and F < 15
+            if one_launch:
+                try:
+                    K.exact_linear_bf16x(x, (wc[0][0], wc[0][2], wc[0][3]), Kd, F, TRUNC, cfg=cfg)
+                except NotImplementedError:
+                    one_launch = False
+            if one_launch:
+                t_gemm = time_graph(lambda r: K.exact_linear_bf16x(x, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, TRUNC,
+                                                                   cfg=cfg), nrot)
+            else:
+                t_gemm = time_graph(lambda r: K.exact_linear_packed(xd, (wc[r][0], wc[r][2], wc[r][3]), Kd, F,
+                                                                    TRUNC, cfg=cfg), nrot)
             t_bf16 = time_graph(lambda r: torch.matmul(x, wbs[r].T), len(wbs))
             t_i8 = None
             if M > 16:
@@ -387,7 +401,7 @@ def main():
                        gemm_TOPS=round(o / t_gemm / 1e6, 1), hbm_frac=round(b / t_gemm / 1e3 / HBM_PEAK_GBS, 3),
                        mfma_frac=round(o / t_gemm / 1e6 / INT8_PEAK_TOPS, 3), roofline_frac=round(t_roof / t_gemm, 3),
                        bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma",
-                       vs_bf16=round(t_op / t_bf16, 2), weight_copies=nrot)
+                       vs_bf16=round(t_op / t_bf16, 2), weight_copies=nrot, one_launch=one_launch)
             per_op[(M, name)] = rec
             log(json.dumps(rec))
         del wc, wbs, b8

@@ -122,6 +122,22 @@ int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, const int32_t* 
                             void* ws, size_t ws_bytes, vxa_stream_t stream);
 
 /*
+ * Digitize x and run vxa_exact_linear_packed in one launch: the same bits as
+ * vxa_digitize_packed followed by vxa_exact_linear_packed, for decode at batch 1-4.
+ *   x    bf16 [m, k], row stride ldx elements; 1 <= m <= 4
+ *   wp, sw  packed weight digits and weight shifts (as vxa_exact_linear_packed); f <= 14
+ *   cfg  a small-M config with a one-row-tile (BM <= 16) and SK = 1
+ * Returns VXA_ERR_UNSUPPORTED for f = 15, m > 4, another cfg family, or x rows that are not
+ * 16-byte aligned: the caller then takes the two-launch path. No reference counterpart: the
+ * reference digitizes x in a launch of its own (plugin.py:62-64); this entry point serves the
+ * exactmm::linear op at batch 1-4, where that launch is a quarter of the op.
+ */
+int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw,
+                           void* out, int out_dtype, int64_t ldo,
+                           int64_t m, int64_t n, int64_t k, int f, int trunc,
+                           const int32_t* cfg, int cfg_len, vxa_stream_t stream);
+
+/*
  * Workspace bytes for vxa_paged_decode: fp32 segment partials m, l [n, H, NS] and
  * acc [n, H, NS, D] with NS = max(1, cdiv(max_len, split)) (paged_attn.py:105-108).
  * Zero when NS == 1 (every request then finishes inside one segment).

@@ -110,3 +110,30 @@ def test_entry_points_validate_before_launching():
     assert call(H=30, KV=8) == nx.VXA_ERR_ARG
     assert call(max_len=4096) == nx.VXA_ERR_WORKSPACE
     assert call(n=0) == nx.VXA_OK
+
+
+def test_fused_entry_point_validates_before_launching():
+    # vxa_exact_linear_bf16x refuses what its one launch does not cover (the op then takes the
+    # two-launch path) and bad arguments, all before any launch: the pointers are never read
+    L = nx.lib()
+    fake = 16
+    sm, sm_n = nx.cfg_array((16, 32, 128, 8, 1, 8, 1))
+
+    def call(m=1, n=4096, k=4096, f=14, cfg=(sm, sm_n), x=fake, ldx=4096, od=nx.VXA_BF16, ldo=4096, w=fake):
+        return L.vxa_exact_linear_bf16x(x, ldx, w, fake, fake, od, ldo, m, n, k, f, 1, cfg[0], cfg[1], None)
+
+    assert call(m=5) == nx.VXA_ERR_UNSUPPORTED  # more rows than the one-launch path takes
+    assert call(f=15) == nx.VXA_ERR_UNSUPPORTED  # offset digits need a row sum first
+    assert call(cfg=nx.cfg_array((64, 96, 64, 6, 6, 8, 1))) == nx.VXA_ERR_UNSUPPORTED  # not a small-M cfg
+    assert call(cfg=nx.cfg_array((32, 32, 128, 8, 1, 8, 1))) == nx.VXA_ERR_UNSUPPORTED  # two row tiles
+    assert call(cfg=nx.cfg_array((16, 32, 128, 8, 1, 8, 2))) == nx.VXA_ERR_UNSUPPORTED  # split-K
+    assert call(x=fake + 2) == nx.VXA_ERR_UNSUPPORTED  # rows not 16-byte aligned
+    assert call(ldx=4100) == nx.VXA_ERR_UNSUPPORTED
+    assert call(k=0) == nx.VXA_ERR_UNSUPPORTED
+    assert call(m=0) == nx.VXA_OK
+    assert call(f=16) == nx.VXA_ERR_ARG
+    assert call(od=9) == nx.VXA_ERR_ARG
+    assert call(ldo=100) == nx.VXA_ERR_ARG
+    assert call(ldx=100) == nx.VXA_ERR_ARG
+    assert call(x=None) == nx.VXA_ERR_ARG
+    assert call(w=fake + 8) == nx.VXA_ERR_ARG

@@ -4,7 +4,8 @@ The packed layout has no counterpart in the reference; tests/helpers.pack_np sta
 independently in numpy. Checks: GPU packing matches it byte for byte; digitize_packed equals
 pack(digitize) and the oracle's digits; the packed GEMM equals the oracle bitwise for every
 kernel family (small-M, LDS ring, x through LDS with weights in registers), ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
-exactmm::linear op on load-time packed weights equals the oracle.
+one-launch digitize + GEMM path at 1-4 rows equals the oracle; the exactmm::linear op on
+load-time packed weights equals the oracle.
 """
 import itertools
 
@@ -60,6 +61,65 @@ def test_packed_gemm_bitwise(F, tr, M, N, Kd):
     K.exact_linear_packed(xp, wp, Kd, F, tr, out=yb, cfg=(16, 64, 128, 4, 1, 8, 2))
     want_b = oracle.bf16_rne_c(oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr)).reshape(M, N)
     assert np.array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), want_b)
+
+
+FUSED_CFGS = tuple((16, 16 * nt, 128, nwk, c, 8, 1) for mt, nt, c, nwk in K.SMALL_SHAPES if mt == 1)
+
+
+@pytest.mark.parametrize("F,tr", [(14, True), (14, False), (12, True)])
+@pytest.mark.parametrize("M,N,Kd", [(1, 64, 4096), (2, 200, 1000), (3, 96, 4104), (4, 48, 64), (4, 16, 12288),
+                                    (1, 130, 40)])
+def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
+    """exact_linear_bf16x (x digitized inside the GEMM launch, M <= 4) gives the oracle's bits
+    for every one-row-tile config, with ragged N and K (K not a multiple of 64 or 16), rows
+    of magnitudes 1e-3 to 1e3 and a zero row; the exactmm::linear op takes this path at
+    1-4 rows and gives the same bits."""
+    x, w = stress_xw(M, N, Kd, seed=M * 7 + Kd)
+    x = (x * (10.0 ** torch.linspace(-3, 3, M))[:, None]).to(torch.bfloat16)
+    if M >= 3:
+        x[1] = 0  # sh = F, zero digits
+    wb = w.to(torch.bfloat16)
+    xd_np = oracle.digitize_c(x.float().numpy(), F)
+    wd_np = oracle.digitize_c(wb.float().numpy(), F)
+    ref32 = oracle.exact_linear_c(xd_np, wd_np, F, tr)
+    wp = K.digitize_packed(wb.to(DEV), F)
+    xg = x.to(DEV)
+    for cfg in FUSED_CFGS:
+        y = K.exact_linear_bf16x(xg, wp, Kd, F, tr, cfg=cfg)
+        assert np.array_equal(f32_bits(y.cpu().numpy()), f32_bits(ref32)), cfg
+    yb = torch.empty(M, N + 8, device=DEV, dtype=torch.bfloat16)[:, :N]  # row stride N + 8
+    K.exact_linear_bf16x(xg, wp, Kd, F, tr, out=yb, cfg=FUSED_CFGS[0])
+    want_b = oracle.bf16_rne_c(ref32).reshape(M, N)
+    assert np.array_equal(yb.cpu().contiguous().view(torch.int16).numpy().view(np.uint16), want_b)
+    if (F, tr) == (plugin.F, plugin.TRUNC):
+        y_op = torch.ops.exactmm.linear(xg, *plugin.pack_weight(wb.to(DEV)))
+        assert np.array_equal(y_op.cpu().view(torch.int16).numpy().view(np.uint16), want_b)
+
+
+def test_fused_path_declines_and_the_op_falls_back():
+    """Where one launch does not apply (F = 15, five rows, x rows not 16-byte aligned, a
+    split-K or wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's
+    two-launch path still gives the oracle's bits."""
+    g = torch.Generator().manual_seed(5)
+    N, Kd = 96, 1001  # K = 1001: bf16 rows of 2002 bytes, not 16-byte aligned
+    w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(5, Kd, generator=g).to(torch.bfloat16)
+    wp = K.digitize_packed(w.to(DEV), 14)
+    xg = x.to(DEV)
+    cfg = FUSED_CFGS[0]
+    for args, kw in (((xg[:2], wp, Kd, 15, False), dict(cfg=cfg)), ((xg, wp, Kd, 14, True), dict(cfg=cfg)),
+                     ((xg[:2], wp, Kd, 14, True), dict(cfg=cfg)),
+                     ((xg[:2], wp, Kd, 14, True), dict(cfg=(16, 32, 128, 8, 1, 8, 2))),
+                     ((xg[:2], wp, Kd, 14, True), dict(cfg=(64, 96, 64, 6, 6, 8, 1)))):
+        with pytest.raises(NotImplementedError):
+            K.exact_linear_bf16x(*args, **kw)
+    wbuf = plugin.pack_weight(w.to(DEV))
+    wd_np = oracle.digitize_c(w.float().numpy(), plugin.F)
+    for M in (2, 5):
+        y = torch.ops.exactmm.linear(xg[:M], *wbuf)
+        ref = oracle.exact_linear_c(oracle.digitize_c(x[:M].float().numpy(), plugin.F), wd_np, plugin.F, plugin.TRUNC)
+        assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16),
+                              oracle.bf16_rne_c(ref).reshape(ref.shape)), M
 
 
 @pytest.mark.parametrize("shape", [(6144, 4096), (24576, 4096), (4096, 12288)])

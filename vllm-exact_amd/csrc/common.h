@@ -50,6 +50,22 @@ __device__ inline float shfl_xor_f32(float v, int mask) {
   return shfl_f32(v, lane ^ mask);
 }
 
+// Row scale of the digitization (kernels.py:25-29): e = frexp exponent of the row absmax
+// (0 for a zero row), sh = F - e, scale = 2^sh built from its exponent bits.
+__device__ inline float digit_scale(float absmax, int F, int& sh) {
+  const int e = (absmax > 0.0f) ? __builtin_amdgcn_frexp_expf(absmax) : 0;
+  sh = F - e;
+  return __uint_as_float((uint32_t)(sh + 127) << 23);
+}
+
+// Balanced digits (F < 15, kernels.py:35-38) of q = trunc(v * scale): q = 256 h + l with
+// l in [-128, 127].
+__device__ inline void digits_balanced(float v, float scale, int32_t& hd, int32_t& ld) {
+  const uint32_t uq = (uint32_t)(int32_t)(v * scale);  // truncation toward zero
+  ld = (int32_t)((uq + 128u) & 255u) - 128;
+  hd = (int32_t)(uq - (uint32_t)ld) >> 8;
+}
+
 // Workgroups are handed to the 8 XCDs round-robin (linear id % 8), and each XCD has its own
 // L2. This bijection gives XCD x the logical ids [x*base + min(x, rem), ...) in dispatch
 // order, so neighbouring logical tiles (which share an operand tile) run on one XCD at about

@@ -133,9 +133,8 @@ __global__ __launch_bounds__(kMaxThreads) void digitize_fast_kernel(const void* 
 #pragma unroll
     for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(v[i][j]));
   a = block_max(a, redf);
-  const int e = (a > 0.0f) ? __builtin_amdgcn_frexp_expf(a) : 0;
-  const int s = F - e;
-  const float scale = __uint_as_float((uint32_t)(s + 127) << 23);
+  int s;
+  const float scale = digit_scale(a, F, s);
 
   uint32_t csum = 0;
 #pragma unroll
@@ -147,14 +146,13 @@ __global__ __launch_bounds__(kMaxThreads) void digitize_fast_kernel(const void* 
     for (int j = 0; j < 16; ++j) {
       int32_t hd = 0, ld = 0;
       if (c * 16 + j < K) {
-        const uint32_t uq = (uint32_t)(int32_t)(v[i][j] * scale);  // truncation toward zero
         if constexpr (OFFSET) {
+          const uint32_t uq = (uint32_t)(int32_t)(v[i][j] * scale);  // truncation toward zero
           ld = (int32_t)(uq & 255u) - 128;
           hd = (int32_t)(uq - (uint32_t)ld - 128u) >> 8;
           csum += (uint32_t)(256 * hd + ld);
         } else {
-          ld = (int32_t)((uq + 128u) & 255u) - 128;
-          hd = (int32_t)(uq - (uint32_t)ld) >> 8;
+          digits_balanced(v[i][j], scale, hd, ld);
         }
       }
       hb[j] = (uint8_t)hd;

@@ -6,7 +6,9 @@
 For each weight shape (N, K) and batch bucket M, every candidate config is run, checked
 bitwise against the first candidate's output (exact integer accumulation makes every
 tiling give the same bits; a mismatch raises), and timed by HIP-graph replay with the
-weights rotated over enough copies to stream past the 256 MB MALL. By default the weights
+weights rotated over enough copies to stream past the 256 MB MALL. At 1-4 rows (packed,
+F < 15) the time is the op's: digitize inside the GEMM launch where the cfg allows it,
+digitize + GEMM otherwise. By default the weights
 are packed at load time and x is digitized packed, as exactmm::linear runs them (--layout
 plain tunes the row-major kernels instead). The fastest config is
 written to {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK]}}; the report also records the
@@ -56,8 +58,16 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
     for M in ms:
         x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
         xd = K.digitize_packed(x, F) if packed else K.digitize(x, F)
+        # at 1-4 rows the op digitizes inside the GEMM launch where the cfg allows it, and
+        # launches digitize and GEMM otherwise: time that, digitize included, for every cfg
+        op_path = packed and M <= K.FUSED_MAX_ROWS and F < 15
 
         def run(i, cfg):
+            if op_path:
+                try:
+                    return K.exact_linear_bf16x(x, wds[i], Kd, F, trunc, cfg=cfg)
+                except NotImplementedError:
+                    return K.exact_linear_packed(K.digitize_packed(x, F), wds[i], Kd, F, trunc, cfg=cfg)
             if packed:
                 return K.exact_linear_packed(xd, wds[i], Kd, F, trunc, cfg=cfg)
             return K.exact_linear(xd, wds[i], F, trunc, cfg=cfg)

@@ -35,6 +35,7 @@ EXPORTED = (
     "vxa_pack_digits",
     "vxa_digitize_packed",
     "vxa_exact_linear_packed",
+    "vxa_exact_linear_bf16x",
     "vxa_paged_decode_workspace",
     "vxa_paged_decode",
 )
@@ -61,6 +62,10 @@ _SIGNATURES = {
         _int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int,
          _vp, _sz, _vp],
+    ),
+    "vxa_exact_linear_bf16x": (
+        _int,
+        [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int, _vp],
     ),
     "vxa_paged_decode_workspace": (_int, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
     "vxa_paged_decode": (

@@ -201,6 +201,42 @@ def exact_linear_packed(xp, wp, K, F, trunc=False, out=None, cfg=None):
     return out
 
 
+FUSED_MAX_ROWS = 4  # rows of x the one-launch digitize + GEMM path takes (vxa_exact_linear_bf16x)
+
+
+def exact_linear_bf16x(x, wp, K, F, trunc=False, out=None, cfg=None):
+    """Digitize x (bf16 [M, K], M <= FUSED_MAX_ROWS) and run exact_linear_packed in one launch:
+    the bits of exact_linear_packed(digitize_packed(x, F), wp, K, F, trunc, cfg=cfg).
+    Raises NotImplementedError where the one-launch path does not apply (F = 15, more rows, a
+    cfg outside the one-row-tile small-M family or with split-K, x rows not 16-byte aligned);
+    the two-launch path covers those."""
+    pw, cw, sw = wp
+    _require_gpu(x, "exact_linear_bf16x")
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("exact_linear_bf16x: x must be a 2-D bf16 tensor with contiguous rows")
+    M, N = x.shape[0], sw.numel()
+    if x.shape[1] != K:
+        raise ValueError(f"exact_linear_bf16x: x has {x.shape[1]} columns, K is {K}")
+    if pw.dtype != torch.int8 or pw.shape != packed_shape(N, K) or not pw.is_contiguous():
+        raise ValueError("exact_linear_bf16x: weights must be contiguous int8 of packed_shape(N, K)")
+    _check_sums("exact_linear_bf16x (w)", cw, sw, N)
+    dev = x.device
+    if any(t.device != dev for t in wp):
+        raise ValueError("exact_linear_bf16x: x and the weights must be on one device")
+    if out is None:
+        out = torch.empty((M, N), device=dev, dtype=torch.float32)
+    if out.shape != (M, N) or out.stride(1) != 1 or out.device != dev:
+        raise ValueError("exact_linear_bf16x: out must be an (M, N) row-major tensor")
+    if cfg is None:
+        raise ValueError("exact_linear_bf16x: pass a cfg (plugin._cfg or a tuning-table entry)")
+    arr, n = _nx.cfg_array(cfg)
+    with torch.cuda.device(dev):
+        _nx.check(_nx.lib().vxa_exact_linear_bf16x(
+            x.data_ptr(), x.stride(0), pw.data_ptr(), sw.data_ptr(), out.data_ptr(), _nx.dtype_enum(out.dtype),
+            out.stride(0), M, N, K, int(F), int(bool(trunc)), arr, n, _nx.stream_handle(dev)), "exact_linear_bf16x")
+    return out
+
+
 # gfx950 kernel shapes, as cfg tuples (BM, BN, BK, warps, stages, GM). Three families:
 # * small-M register-streaming kernel: BM = 16*MT rows, BN = 16*NT columns per workgroup,
 #   `warps` waves splitting K, `stages` = K steps whose loads are issued together;
@@ -318,4 +354,4 @@ def autotune_exact(xd, wd, F, trunc):
 
 __all__ = ["HAVE_HIP", "HAVE_TRITON", "digitize_torch", "digitize_weight", "digitize", "exact_linear_torch",
            "exact_linear", "autotune_exact", "EXACT_CFGS", "pack_digits", "digitize_packed", "exact_linear_packed",
-           "packed_shape"]
+           "packed_shape", "exact_linear_bf16x", "FUSED_MAX_ROWS"]
