@@ -371,9 +371,9 @@ def main():
             x = xs[(M, Kd)]
             xd = K.digitize_packed(x, F)
             t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
-            # the GEMM kernel the op runs: at 1-4 rows the one-launch digitize + GEMM kernel
-            # (x read as bf16), otherwise the GEMM on digits digitized beforehand
-            one_launch = M <= K.FUSED_MAX_ROWS and F < 15
+            # the GEMM kernel the op runs: at 1-4 rows the one-launch digitize + GEMM kernel (x
+            # read as bf16), otherwise the GEMM on digits digitized beforehand
+            one_launch = F < 15 and M <= K.ONE_LAUNCH_MAX_ROWS
             if one_launch:
                 try:
                     K.exact_linear_bf16x(x, (wc[0][0], wc[0][2], wc[0][3]), Kd, F, TRUNC, cfg=cfg)

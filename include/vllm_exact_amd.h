@@ -123,14 +123,15 @@ int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, const int32_t* 
 
 /*
  * Digitize x and run vxa_exact_linear_packed in one launch: the same bits as
- * vxa_digitize_packed followed by vxa_exact_linear_packed, for decode at batch 1-4.
- *   x    bf16 [m, k], row stride ldx elements; 1 <= m <= 4
+ * vxa_digitize_packed followed by vxa_exact_linear_packed.
+ *   x    bf16 [m, k], row stride ldx elements
  *   wp, sw  packed weight digits and weight shifts (as vxa_exact_linear_packed); f <= 14
- *   cfg  a small-M config with a one-row-tile (BM <= 16) and SK = 1
- * Returns VXA_ERR_UNSUPPORTED for f = 15, m > 4, another cfg family, or x rows that are not
- * 16-byte aligned: the caller then takes the two-launch path. No reference counterpart: the
- * reference digitizes x in a launch of its own (plugin.py:62-64); this entry point serves the
- * exactmm::linear op at batch 1-4, where that launch is a quarter of the op.
+ *   cfg  a small-M config with one-row tiles (BM <= 16) and SK = 1
+ * Each workgroup digitizes its own 16 rows of x (row absmax over k, then the digits in
+ * registers). Returns VXA_ERR_UNSUPPORTED for f = 15, another cfg family, or x rows that are
+ * not 16-byte aligned: the caller then takes the two-launch path. No reference counterpart:
+ * the reference digitizes x in a launch of its own (plugin.py:62-64); this entry point serves
+ * the exactmm::linear op at decode sizes, where that launch is a quarter of the op.
  */
 int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw,
                            void* out, int out_dtype, int64_t ldo,

@@ -68,12 +68,12 @@ FUSED_CFGS = tuple((16, 16 * nt, 128, nwk, c, 8, 1) for mt, nt, c, nwk in K.SMAL
 
 @pytest.mark.parametrize("F,tr", [(14, True), (14, False), (12, True)])
 @pytest.mark.parametrize("M,N,Kd", [(1, 64, 4096), (2, 200, 1000), (3, 96, 4104), (4, 48, 64), (4, 16, 12288),
-                                    (1, 130, 40)])
+                                    (1, 130, 40), (16, 64, 4096), (37, 80, 1000), (64, 48, 12288), (20, 32, 8)])
 def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
-    """exact_linear_bf16x (x digitized inside the GEMM launch, M <= 4) gives the oracle's bits
-    for every one-row-tile config, with ragged N and K (K not a multiple of 64 or 16), rows
-    of magnitudes 1e-3 to 1e3 and a zero row; the exactmm::linear op takes this path at
-    1-4 rows and gives the same bits."""
+    """exact_linear_bf16x (x digitized inside the GEMM launch, each workgroup its own 16 rows)
+    gives the oracle's bits for every one-row-tile config, with ragged M, N and K (K not a
+    multiple of 64, 16 or 8), rows of magnitudes 1e-3 to 1e3 and a zero row; the
+    exactmm::linear op takes this path and gives the same bits."""
     x, w = stress_xw(M, N, Kd, seed=M * 7 + Kd)
     x = (x * (10.0 ** torch.linspace(-3, 3, M))[:, None]).to(torch.bfloat16)
     if M >= 3:
@@ -97,9 +97,9 @@ def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
 
 
 def test_fused_path_declines_and_the_op_falls_back():
-    """Where one launch does not apply (F = 15, five rows, x rows not 16-byte aligned, a
-    split-K or wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's
-    two-launch path still gives the oracle's bits."""
+    """Where one launch does not apply (F = 15, x rows not 16-byte aligned, a split-K or
+    wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's two-launch path
+    still gives the oracle's bits."""
     g = torch.Generator().manual_seed(5)
     N, Kd = 96, 1001  # K = 1001: bf16 rows of 2002 bytes, not 16-byte aligned
     w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)
@@ -107,8 +107,7 @@ def test_fused_path_declines_and_the_op_falls_back():
     wp = K.digitize_packed(w.to(DEV), 14)
     xg = x.to(DEV)
     cfg = FUSED_CFGS[0]
-    for args, kw in (((xg[:2], wp, Kd, 15, False), dict(cfg=cfg)), ((xg, wp, Kd, 14, True), dict(cfg=cfg)),
-                     ((xg[:2], wp, Kd, 14, True), dict(cfg=cfg)),
+    for args, kw in (((xg[:2], wp, Kd, 15, False), dict(cfg=cfg)), ((xg[:2], wp, Kd, 14, True), dict(cfg=cfg)),
                      ((xg[:2], wp, Kd, 14, True), dict(cfg=(16, 32, 128, 8, 1, 8, 2))),
                      ((xg[:2], wp, Kd, 14, True), dict(cfg=(64, 96, 64, 6, 6, 8, 1)))):
         with pytest.raises(NotImplementedError):

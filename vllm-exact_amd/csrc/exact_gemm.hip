@@ -226,7 +226,7 @@ extern "C" int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* 
                                       const int32_t* cfg, int cfg_len, vxa_stream_t stream) {
   if (m < 0 || n < 0 || k < 0 || f < 1 || f > 15) return VXA_ERR_ARG;
   if (out_dtype != VXA_F32 && out_dtype != VXA_BF16 && out_dtype != VXA_F16) return VXA_ERR_ARG;
-  if (f == 15 || m > exact_fused_max_rows()) return VXA_ERR_UNSUPPORTED;  // offset digits need a row sum first
+  if (f == 15) return VXA_ERR_UNSUPPORTED;  // offset digits need a row sum first
   ExactPlan pl;
   const int rc = make_plan(cdiv<int64_t>(k, 64) * 64, cfg, cfg_len, &pl);
   if (rc != VXA_OK) return rc;

@@ -1,12 +1,12 @@
-// Digitize + exact GEMM in one launch for decode at batch 1-4 (M <= 4 rows of bf16 x, packed
-// weights, F <= 14).
+// Digitize + exact GEMM in one launch: bf16 x, packed weights, F <= 14, the small-M kernel's
+// one-row-tile shapes (16 rows of x per workgroup).
 //
-// The two-launch path runs the digitize kernel (one workgroup per row) and then the small-M
-// GEMM; at M = 1 the second launch and the wait between them are a quarter of the op. Here
+// The two-launch path runs the digitize kernel (one workgroup per row) and then the GEMM; at
+// decode sizes the second launch and the wait between them are a quarter of the op. Here
 // every GEMM workgroup digitizes the x it needs itself:
-//   1. the row absmax of the M rows over all of K (a few KiB of L2-resident bf16 per
-//      workgroup), reduced across the workgroup, gives each row's scale (digit_scale, the
-//      digitize kernels' own helper);
+//   1. the absmax of each of its 16 rows over all of K (16 * K * 2 bytes of L2-resident bf16;
+//      one wave per row, each lane's loads batched so a row costs one or two L2 round trips)
+//      gives each row's scale (digit_scale, the digitize kernels' own helper);
 //   2. in the K loop, a lane reads its 16 bf16 columns of its row straight from x and splits
 //      them into the two MFMA digit operands (digits_balanced) in registers;
 //   3. MFMAs, wave partials and the epilogue are the small-M kernel's (exact_gemm_sm.hip).
@@ -16,8 +16,6 @@
 #include "exact_gemm_common.h"
 
 namespace {
-
-constexpr int kFusedMaxRows = 4;
 
 struct FusedParams {
   const uint16_t* x;  // bf16 [M, K], row stride ldx elements
@@ -34,29 +32,34 @@ struct FusedParams {
 template <int NT, int NWK, int C, bool TRUNC>
 __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
   constexpr int BN = 16 * NT;
+  constexpr int RPW = (16 + NWK - 1) / NWK;  // tile rows each wave reduces in the row pass
+  constexpr int PB = 8;                      // row-pass loads per lane in flight (full tiles)
   __shared__ unsigned long long red[16 * BN];
-  __shared__ float s_max[NWK][kFusedMaxRows];
-  __shared__ float s_scale[kFusedMaxRows];
-  __shared__ int32_t s_sh[kFusedMaxRows];
+  __shared__ float s_scale[16];
+  __shared__ int32_t s_sh[16];
+  __shared__ float s_max[NWK][4];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
   const int nthr = 64 * NWK;
-  const int64_t n0 = (int64_t)blockIdx.x * BN;
-  const int M = (int)p.M;
+  const int64_t nbn = cdiv<int64_t>(p.N, BN);
+  const int64_t bn = blockIdx.x % nbn;
+  const int64_t m0 = (int64_t)(blockIdx.x / nbn) * 16;
+  const int64_t n0 = bn * BN;
+  const int mrows = (int)min<int64_t>(16, p.M - m0);  // rows of this tile below M
 
   for (int i = threadIdx.x; i < 16 * BN; i += nthr) red[i] = 0ull;
 
   // Operand addressing.
-  const bool row_ok = r16 < M;
+  const bool row_ok = r16 < mrows;
   float scale = 0.0f;  // this lane's row scale, set after the row-absmax pass
-  const uint16_t* xrow = p.x + (int64_t)(row_ok ? r16 : 0) * p.ldx + kq * 16;
+  const uint16_t* xrow = p.x + (m0 + (row_ok ? r16 : 0)) * p.ldx + kq * 16;
   const int8_t* whp[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int64_t tile = min((int64_t)blockIdx.x * NT + nt, cdiv<int64_t>(p.N, 16) - 1);
+    const int64_t tile = min(bn * NT + nt, cdiv<int64_t>(p.N, 16) - 1);
     whp[nt] = p.wp + tile * p.KT * 2048 + lane * 16;
   }
   // x of this lane's 16 columns of K step s; zero past K and for rows past M. The last step
@@ -111,41 +114,116 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
     mx[nt] = v4i{0, 0, 0, 0};
     ll[nt] = v4i{0, 0, 0, 0};
   }
-  // 1. Row absmax of the M rows: each thread takes 8-column chunks (one 16-byte load each).
-  float amax[kFusedMaxRows];
+  // 1. Row absmax over all of K, in 8-column chunks (one 16-byte load each); the last K % 8
+  // columns of a row are read per element. A tile of up to 4 rows (decode) spreads each row
+  // over the whole workgroup and meets in LDS; a fuller tile gives each wave its own rows
+  // (w, w + NWK, ...), its items (row j, chunk c) = j * cpr + c going to the lanes in turn
+  // with PB loads per lane in flight.
+  const int cpr = (int)(p.K / 8);  // whole chunks per row
+  if (mrows <= 4) {
+    float amax[4];
 #pragma unroll
-  for (int r = 0; r < kFusedMaxRows; ++r) {
-    amax[r] = 0.0f;
-    if (r < M) {
-      const uint16_t* row = p.x + (int64_t)r * p.ldx;
-      for (int64_t c = threadIdx.x; c * 8 < p.K; c += nthr) {
-        if (c * 8 + 8 <= p.K) {
-          const uint4 u = *reinterpret_cast<const uint4*>(row + c * 8);
-          const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    for (int j = 0; j < 4; ++j) amax[j] = 0.0f;
+    const int items = mrows * cpr;
+    for (int base = threadIdx.x; base < items; base += nthr * 4) {
+      uint4 u[4];
+      int jr[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            amax[r] = fmaxf(amax[r], fabsf(__uint_as_float(w[e] << 16)));
-            amax[r] = fmaxf(amax[r], fabsf(__uint_as_float(w[e] & 0xFFFF0000u)));
-          }
-        } else {
-          for (int64_t k = c * 8; k < p.K; ++k) amax[r] = fmaxf(amax[r], fabsf(bf16_to_f32(row[k])));
+      for (int q = 0; q < 4; ++q) {
+        const int it = base + nthr * q;
+        jr[q] = -1;
+        if (it < items) {
+          jr[q] = it / cpr;
+          u[q] = *reinterpret_cast<const uint4*>(p.x + (m0 + jr[q]) * p.ldx + (int64_t)(it % cpr) * 8);
         }
       }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (jr[q] < 0) continue;
+        const uint32_t w[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          m = fmaxf(m, fabsf(__uint_as_float(w[e] << 16)));
+          m = fmaxf(m, fabsf(__uint_as_float(w[e] & 0xFFFF0000u)));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j == jr[q]) amax[j] = fmaxf(amax[j], m);
+      }
     }
-  }
+    for (int it = threadIdx.x; it < mrows * (int)(p.K - (int64_t)cpr * 8); it += nthr) {
+      const int tail = (int)(p.K - (int64_t)cpr * 8);
+      const int j = it / tail;
+      const float v = fabsf(bf16_to_f32(p.x[(m0 + j) * p.ldx + (int64_t)cpr * 8 + it % tail]));
 #pragma unroll
-  for (int r = 0; r < kFusedMaxRows; ++r) {
+      for (int jj = 0; jj < 4; ++jj)
+        if (jj == j) amax[jj] = fmaxf(amax[jj], v);
+    }
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) amax[r] = fmaxf(amax[r], shfl_xor_f32(amax[r], m));
-    if (lane == 0) s_max[wave][r] = amax[r];
-  }
-  __syncthreads();
-  if (threadIdx.x < kFusedMaxRows) {
-    float a = 0.0f;
-    for (int w = 0; w < NWK; ++w) a = fmaxf(a, s_max[w][threadIdx.x]);
-    int sh;
-    s_scale[threadIdx.x] = digit_scale(a, p.F, sh);
-    s_sh[threadIdx.x] = sh;
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) amax[j] = fmaxf(amax[j], shfl_xor_f32(amax[j], m));
+      if (lane == 0) s_max[wave][j] = amax[j];
+    }
+    __syncthreads();
+    if (threadIdx.x < mrows) {
+      float a = 0.0f;
+      for (int w = 0; w < NWK; ++w) a = fmaxf(a, s_max[w][threadIdx.x]);
+      int sh;
+      s_scale[threadIdx.x] = digit_scale(a, p.F, sh);
+      s_sh[threadIdx.x] = sh;
+    }
+  } else {
+    int nrw = 0;  // rows this wave reduces
+#pragma unroll
+    for (int j = 0; j < RPW; ++j)
+      if (wave + NWK * j < mrows) nrw = j + 1;
+    float amax[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) amax[j] = 0.0f;
+    const int items = nrw * cpr;
+    for (int base = lane; base < items; base += 64 * PB) {
+      uint4 u[PB];
+      int jr[PB];
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        const int it = base + 64 * q;
+        jr[q] = -1;
+        if (it < items) {
+          jr[q] = it / cpr;
+          u[q] = *reinterpret_cast<const uint4*>(p.x + (m0 + wave + NWK * jr[q]) * p.ldx + (int64_t)(it % cpr) * 8);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        if (jr[q] < 0) continue;
+        const uint32_t w[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          m = fmaxf(m, fabsf(__uint_as_float(w[e] << 16)));
+          m = fmaxf(m, fabsf(__uint_as_float(w[e] & 0xFFFF0000u)));
+        }
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+          if (j == jr[q]) amax[j] = fmaxf(amax[j], m);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+      if (j < nrw) {
+        const uint16_t* row = p.x + (m0 + wave + NWK * j) * p.ldx;
+        for (int64_t k = (int64_t)cpr * 8 + lane; k < p.K; k += 64) amax[j] = fmaxf(amax[j], fabsf(bf16_to_f32(row[k])));
+      }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) amax[j] = fmaxf(amax[j], shfl_xor_f32(amax[j], m));
+      if (lane == 0 && j < nrw) {
+        int sh;
+        s_scale[wave + NWK * j] = digit_scale(amax[j], p.F, sh);
+        s_sh[wave + NWK * j] = sh;
+      }
+    }
   }
   __syncthreads();
   scale = s_scale[row_ok ? r16 : 0];
@@ -207,20 +285,20 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
       int64_t tot = ((int64_t)hh[nt][r] << 16) + (cross << 8);
       if constexpr (!TRUNC) tot += (int64_t)ll[nt][r];
       const int m = kq * 4 + r;
-      if (m < M) atomicAdd(&red[m * BN + nt * 16 + r16], (unsigned long long)tot);
+      if (m < mrows) atomicAdd(&red[m * BN + nt * 16 + r16], (unsigned long long)tot);
     }
   __syncthreads();
-  for (int i = threadIdx.x; i < M * BN; i += nthr) {
+  for (int i = threadIdx.x; i < mrows * BN; i += nthr) {
     const int m = i / BN;
     const int64_t n = n0 + i % BN;
     if (n < p.N)
-      store_f32_as(p.out, p.out_dtype, m * p.ldo + n, exact_epilogue((int64_t)red[i], s_sh[m], p.sw[n]));
+      store_f32_as(p.out, p.out_dtype, (m0 + m) * p.ldo + n, exact_epilogue((int64_t)red[i], s_sh[m], p.sw[n]));
   }
 }
 
 template <int NT, int NWK, int C, bool TRUNC>
 hipError_t launch(const FusedParams& fp, hipStream_t st) {
-  const int64_t blocks = cdiv<int64_t>(fp.N, 16 * NT);
+  const int64_t blocks = cdiv<int64_t>(fp.M, 16) * cdiv<int64_t>(fp.N, 16 * NT);
   if (blocks > 0x7FFFFFFFLL) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC>), dim3((unsigned)blocks), dim3(64 * NWK), 0, st, fp);
   return hipGetLastError();
@@ -242,8 +320,6 @@ hipError_t dispatch(const ExactPlan& pl, const FusedParams& fp, hipStream_t st) 
 }
 
 }  // namespace
-
-int exact_fused_max_rows() { return kFusedMaxRows; }
 
 hipError_t launch_exact_fused(const ExactPlan& pl, const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw,
                               void* out, int out_dtype, int64_t ldo, int64_t m, int64_t n, int64_t k, int f,

@@ -6,9 +6,9 @@
 For each weight shape (N, K) and batch bucket M, every candidate config is run, checked
 bitwise against the first candidate's output (exact integer accumulation makes every
 tiling give the same bits; a mismatch raises), and timed by HIP-graph replay with the
-weights rotated over enough copies to stream past the 256 MB MALL. At 1-4 rows (packed,
-F < 15) the time is the op's: digitize inside the GEMM launch where the cfg allows it,
-digitize + GEMM otherwise. By default the weights
+weights rotated over enough copies to stream past the 256 MB MALL. At 1-4 rows on packed
+weights with F < 15 the time is the op's: digitize inside the GEMM launch where the cfg
+allows it, digitize + GEMM otherwise. By default the weights
 are packed at load time and x is digitized packed, as exactmm::linear runs them (--layout
 plain tunes the row-major kernels instead). The fastest config is
 written to {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK]}}; the report also records the
@@ -60,7 +60,7 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
         xd = K.digitize_packed(x, F) if packed else K.digitize(x, F)
         # at 1-4 rows the op digitizes inside the GEMM launch where the cfg allows it, and
         # launches digitize and GEMM otherwise: time that, digitize included, for every cfg
-        op_path = packed and M <= K.FUSED_MAX_ROWS and F < 15
+        op_path = packed and F < 15 and M <= K.ONE_LAUNCH_MAX_ROWS
 
         def run(i, cfg):
             if op_path:

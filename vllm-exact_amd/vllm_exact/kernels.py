@@ -201,15 +201,23 @@ def exact_linear_packed(xp, wp, K, F, trunc=False, out=None, cfg=None):
     return out
 
 
-FUSED_MAX_ROWS = 4  # rows of x the one-launch digitize + GEMM path takes (vxa_exact_linear_bf16x)
+# The exactmm::linear op digitizes inside the GEMM launch (exact_linear_bf16x) up to this many
+# rows. Measured on MI355X: the one launch saves 2-6 µs per op at 1-4 rows; at 16 rows the
+# workgroups' own row pass costs what the digitize launch does, and at 64 it costs more.
+ONE_LAUNCH_MAX_ROWS = 4
+
+
+def bf16x_rows_aligned(x):
+    """True when x's rows can be read 16 bytes at a time (what exact_linear_bf16x needs)."""
+    return x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0
 
 
 def exact_linear_bf16x(x, wp, K, F, trunc=False, out=None, cfg=None):
-    """Digitize x (bf16 [M, K], M <= FUSED_MAX_ROWS) and run exact_linear_packed in one launch:
-    the bits of exact_linear_packed(digitize_packed(x, F), wp, K, F, trunc, cfg=cfg).
-    Raises NotImplementedError where the one-launch path does not apply (F = 15, more rows, a
-    cfg outside the one-row-tile small-M family or with split-K, x rows not 16-byte aligned);
-    the two-launch path covers those."""
+    """Digitize x (bf16 [M, K]) and run exact_linear_packed in one launch: the bits of
+    exact_linear_packed(digitize_packed(x, F), wp, K, F, trunc, cfg=cfg). Raises
+    NotImplementedError where the one-launch path does not apply (F = 15, a cfg outside the
+    one-row-tile small-M family or with split-K, x rows not 16-byte aligned); the two-launch
+    path covers those."""
     pw, cw, sw = wp
     _require_gpu(x, "exact_linear_bf16x")
     if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
@@ -354,4 +362,4 @@ def autotune_exact(xd, wd, F, trunc):
 
 __all__ = ["HAVE_HIP", "HAVE_TRITON", "digitize_torch", "digitize_weight", "digitize", "exact_linear_torch",
            "exact_linear", "autotune_exact", "EXACT_CFGS", "pack_digits", "digitize_packed", "exact_linear_packed",
-           "packed_shape", "exact_linear_bf16x", "FUSED_MAX_ROWS"]
+           "packed_shape", "exact_linear_bf16x", "bf16x_rows_aligned", "ONE_LAUNCH_MAX_ROWS"]

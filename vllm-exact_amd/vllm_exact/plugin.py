@@ -62,12 +62,17 @@ def _cfg(M, N, Kd):
     return LARGE_M_CFG
 
 
+# cfgs the one-launch digitize + GEMM path refused (two-row tiles, split-K, other families)
+_ONE_LAUNCH_CFG = {}
+
+
 @torch.library.custom_op("exactmm::linear", mutates_args=())
 def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: torch.Tensor,
                     sw: torch.Tensor) -> torch.Tensor:
     """y = x @ W^T through the exact path: reshape to 2-D, digitize x (bf16 read directly),
     exact matmul straight into an x.dtype output, in row blocks of RB (plugin.py:51-64). With
-    packed weights and 1-4 bf16 rows, digitize and GEMM share one launch (same bits).
+    packed weights, 1-4 bf16 rows and a one-row-tile cfg, digitize and GEMM share one launch
+    (same bits).
 
     Weights come either as the reference's row-major digit planes wh, wl [N, K], or packed
     at load time (wh = packed [cdiv(N,16), cdiv(K,64), 2, 1024], wl empty); N is sw's length
@@ -84,13 +89,15 @@ def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: tor
         xb = x2[i:i + RB]
         cfg = _cfg(xb.shape[0], N, Kd)
         if packed:
-            if xb.shape[0] <= K.FUSED_MAX_ROWS and xb.dtype == torch.bfloat16 and F < 15:
-                # batch 1-4: digitize inside the GEMM launch (same bits, one launch fewer)
+            if (xb.shape[0] <= K.ONE_LAUNCH_MAX_ROWS and xb.dtype == torch.bfloat16 and F < 15
+                    and _ONE_LAUNCH_CFG.get(cfg, True)):
+                # digitize inside the GEMM launch where the cfg allows it (same bits, one launch fewer)
                 try:
                     K.exact_linear_bf16x(xb, (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
                     continue
                 except NotImplementedError:
-                    pass
+                    if K.bf16x_rows_aligned(xb):
+                        _ONE_LAUNCH_CFG[cfg] = False  # refused for the cfg, not for this x
             K.exact_linear_packed(K.digitize_packed(xb, F), (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
         else:
             K.exact_linear(K.digitize(xb, F), (wh, wl, cw, sw), F, TRUNC, out=out[i:i + RB], cfg=cfg)
