@@ -126,10 +126,12 @@ int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, const int32_t* 
  * vxa_digitize_packed followed by vxa_exact_linear_packed.
  *   x    bf16 [m, k], row stride ldx elements
  *   wp, sw  packed weight digits and weight shifts (as vxa_exact_linear_packed); f <= 14
- *   cfg  a small-M config with one-row tiles (BM <= 16) and SK = 1
+ *   cfg  a small-M config with one-row tiles (BM <= 16) and SK = 1; k <= 32768, so that the
+ *        plan keeps one K split (int32 digit sums stay exact)
  * Each workgroup digitizes its own 16 rows of x (row absmax over k, then the digits in
- * registers). Returns VXA_ERR_UNSUPPORTED for f = 15, another cfg family, or x rows that are
- * not 16-byte aligned: the caller then takes the two-launch path. No reference counterpart:
+ * registers). Returns VXA_ERR_UNSUPPORTED for f = 15, another cfg family, a plan with more
+ * than one K split, or x rows that are not 16-byte aligned: the caller then takes the
+ * two-launch path. No reference counterpart:
  * the reference digitizes x in a launch of its own (plugin.py:62-64); this entry point serves
  * the exactmm::linear op at decode sizes, where that launch is a quarter of the op.
  */

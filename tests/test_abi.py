@@ -129,6 +129,7 @@ def test_fused_entry_point_validates_before_launching():
     assert call(x=fake + 2) == nx.VXA_ERR_UNSUPPORTED  # rows not 16-byte aligned
     assert call(ldx=4100) == nx.VXA_ERR_UNSUPPORTED
     assert call(k=0) == nx.VXA_ERR_UNSUPPORTED
+    assert call(k=40000, ldx=40000) == nx.VXA_ERR_UNSUPPORTED  # two K splits (32768 per split)
     assert call(m=0) == nx.VXA_OK
     assert call(f=16) == nx.VXA_ERR_ARG
     assert call(od=9) == nx.VXA_ERR_ARG
