@@ -29,7 +29,8 @@ struct FusedParams {
   int64_t M, N, K, KT;
 };
 
-template <int NT, int NWK, int C, bool TRUNC>
+// FEW: M <= 4, one tile of at most 4 rows (decode); its row pass is the only one compiled in.
+template <int NT, int NWK, int C, bool TRUNC, bool FEW>
 __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
   constexpr int BN = 16 * NT;
   constexpr int RPW = (16 + NWK - 1) / NWK;  // tile rows each wave reduces in the row pass
@@ -116,11 +117,11 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
   }
   // 1. Row absmax over all of K, in 8-column chunks (one 16-byte load each); the last K % 8
   // columns of a row are read per element. A tile of up to 4 rows (decode) spreads each row
-  // over the whole workgroup and meets in LDS; a fuller tile gives each wave its own rows
+  // over the whole workgroup and meets in LDS; otherwise each wave takes its own rows
   // (w, w + NWK, ...), its items (row j, chunk c) = j * cpr + c going to the lanes in turn
   // with PB loads per lane in flight.
   const int cpr = (int)(p.K / 8);  // whole chunks per row
-  if (mrows <= 4) {
+  if constexpr (FEW) {
     float amax[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) amax[j] = 0.0f;
@@ -300,7 +301,12 @@ template <int NT, int NWK, int C, bool TRUNC>
 hipError_t launch(const FusedParams& fp, hipStream_t st) {
   const int64_t blocks = cdiv<int64_t>(fp.M, 16) * cdiv<int64_t>(fp.N, 16 * NT);
   if (blocks > 0x7FFFFFFFLL) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC>), dim3((unsigned)blocks), dim3(64 * NWK), 0, st, fp);
+  if (fp.M <= 4)
+    hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, true>), dim3((unsigned)blocks), dim3(64 * NWK), 0, st,
+                       fp);
+  else
+    hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, false>), dim3((unsigned)blocks), dim3(64 * NWK), 0,
+                       st, fp);
   return hipGetLastError();
 }
 
