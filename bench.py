@@ -15,8 +15,8 @@ sit in HBM before timing starts. `value` is the sweep's algorithmic bytes
 Also reported, from the same run:
 * per-op times with GB/s, TOPS and roofline fractions, the hipBLASLt bf16 time and, for
   M > 16, the vendor int8 GEMM (torch._int_mm, one dot) on the same shape; `gemm_us` is the
-  kernel the op runs without the digitize launch (at 1-4 rows the one-launch digitize + GEMM
-  kernel, `one_launch`);
+  kernel the op runs without the digitize launch (the one-launch digitize + GEMM kernel at the
+  row counts the table marks, `one_launch`);
 * `roofline` of the dominant kernel (the GEMM launch with the largest share of the step),
   timed alone with HIP events on its own stream;
 * split-bf16 paged decode attention at H=32/KV=8/D=128/BS=16 for 64x8K, 16x16K, 256x1K (TB/s);
@@ -371,9 +371,9 @@ def main():
             x = xs[(M, Kd)]
             xd = K.digitize_packed(x, F)
             t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
-            # the GEMM kernel the op runs: at 1-4 rows the one-launch digitize + GEMM kernel (x
-            # read as bf16), otherwise the GEMM on digits digitized beforehand
-            one_launch = F < 15 and M <= K.ONE_LAUNCH_MAX_ROWS
+            # the GEMM kernel the op runs: where the table marks the row count, the one-launch
+            # digitize + GEMM kernel (x read as bf16), otherwise the GEMM on digits digitized beforehand
+            one_launch = F < 15 and plugin._one_launch(M, N, Kd)
             if one_launch:
                 try:
                     K.exact_linear_bf16x(x, (wc[0][0], wc[0][2], wc[0][3]), Kd, F, TRUNC, cfg=cfg)

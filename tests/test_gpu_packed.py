@@ -4,8 +4,9 @@ The packed layout has no counterpart in the reference; tests/helpers.pack_np sta
 independently in numpy. Checks: GPU packing matches it byte for byte; digitize_packed equals
 pack(digitize) and the oracle's digits; the packed GEMM equals the oracle bitwise for every
 kernel family (small-M, LDS ring, x through LDS with weights in registers), ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
-one-launch digitize + GEMM path at 1-4 rows equals the oracle; the exactmm::linear op on
-load-time packed weights equals the oracle.
+one-launch digitize + GEMM path equals the oracle at 1-64 rows; the exactmm::linear op on
+load-time packed weights, with and without the shipped table (which picks the one-launch
+path at 16 rows for some shapes and not for others), equals the oracle.
 """
 import itertools
 
@@ -14,6 +15,7 @@ import pytest
 import torch
 
 import oracle
+import vllm_exact
 from helpers import f32_bits, np_digits, pack_np, stress_xw, xw
 from vllm_exact import kernels as K
 from vllm_exact import plugin
@@ -128,14 +130,20 @@ def test_op_with_packed_weights_matches_oracle(shape):
     w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)
     wbuf = plugin.pack_weight(w.to(DEV))
     wd_np = oracle.digitize_c(w.float().numpy(), plugin.F)
-    for M in (1, 16, 64, 256):
-        x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
-        y = torch.ops.exactmm.linear(x.to(DEV), *wbuf)
-        rows = np.arange(M) if M <= 64 else np.array([0, 100, 255])
-        xd_np = oracle.digitize_c(x.float().numpy()[rows], plugin.F)
-        ref = oracle.exact_linear_c(xd_np, wd_np, plugin.F, plugin.TRUNC)
-        got = y.cpu().view(torch.int16).numpy().view(np.uint16)[rows]
-        assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape)), M
+    for table in (None, vllm_exact.TABLES["mi355x"]):
+        plugin.load_table(table)
+        try:
+            for M in (1, 16, 64, 256):
+                x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+                y = torch.ops.exactmm.linear(x.to(DEV), *wbuf)
+                rows = np.arange(M) if M <= 64 else np.array([0, 100, 255])
+                xd_np = oracle.digitize_c(x.float().numpy()[rows], plugin.F)
+                ref = oracle.exact_linear_c(xd_np, wd_np, plugin.F, plugin.TRUNC)
+                got = y.cpu().view(torch.int16).numpy().view(np.uint16)[rows]
+                assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape)), (M, table,
+                                                                                         plugin._one_launch(M, N, Kd))
+        finally:
+            plugin.load_table(None)
 
 
 def test_op_row_blocks_and_input_layouts():

@@ -36,6 +36,45 @@ def test_table_bucket_lookup(tmp_path):
     assert plugin._cfg(4096, 4096, 4096) == plugin.LARGE_M_CFG
 
 
+def test_one_launch_marks(tmp_path):
+    # a row's "one_launch" list names the tuned row counts whose calls digitize inside the GEMM
+    # launch, looked up like the cfg (smallest tuned M >= M); rows without one keep M <= 4
+    table = {"4096,4096": {"1": [16, 16, 128, 16, 1, 8, 1], "16": [16, 16, 128, 16, 1, 8, 1],
+                           "64": [32, 32, 128, 8, 2, 8, 1], "one_launch": [16]},
+             "4096,12288": {"1": [16, 16, 128, 16, 1, 8, 1], "16": [16, 16, 128, 8, 2, 8, 1]}}
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(table))
+    plugin.load_table(path)
+    try:
+        assert plugin._cfg(16, 4096, 4096) == (16, 16, 128, 16, 1, 8, 1)  # the list is no M row
+        assert [plugin._one_launch(m, 4096, 4096) for m in (1, 2, 16, 17, 64, 65)] == [
+            False, True, True, False, False, False]
+        assert [plugin._one_launch(m, 4096, 12288) for m in (1, 4, 5, 16)] == [True, True, False, False]
+        assert plugin._one_launch(4, 6144, 4096) and not plugin._one_launch(5, 6144, 4096)
+    finally:
+        plugin.load_table(None)
+    assert plugin._one_launch(4, 4096, 4096) and not plugin._one_launch(16, 4096, 4096)
+
+
+def test_tuner_merge_keeps_untuned_entries():
+    import importlib.util
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("tune_mod", root / "vllm-exact_amd" / "tune_table.py")
+    tune = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(tune)
+    a, b, c = [16, 16, 128, 16, 1, 8, 1], [16, 32, 128, 8, 1, 8, 1], [64, 64, 128, 4, 4, 8, 1]
+    # a base row without marks meant 1-4 rows: entries not retuned keep that meaning
+    old = {"1": a, "4": a, "16": a, "256": c}
+    got = tune.merge_row(old, {"16": b, "one_launch": [16]}, [16])
+    assert got == {"1": a, "4": a, "16": b, "256": c, "one_launch": [1, 4, 16]}
+    got = tune.merge_row(got, {"1": b, "4": b, "one_launch": [4]}, [1, 4])
+    assert got == {"1": b, "4": b, "16": b, "256": c, "one_launch": [4, 16]}
+    # a retune without marks (plain layout) leaves the base's marks alone
+    assert tune.merge_row(got, {"256": a}, [256])["one_launch"] == [4, 16]
+    assert tune.merge_row({}, {"64": c, "one_launch": []}, [64]) == {"64": c, "one_launch": []}
+
+
 def test_shipped_table_is_well_formed():
     path = vllm_exact.TABLES["mi355x"]
     raw = json.loads(path.read_text())
@@ -43,6 +82,9 @@ def test_shipped_table_is_well_formed():
         n, k = map(int, nk.split(","))
         assert n > 0 and k > 0
         for m, cfg in row.items():
+            if m == "one_launch":
+                assert all(str(r) in row for r in cfg), (nk, cfg)  # marks name tuned rows
+                continue
             assert int(m) > 0 and 7 <= len(cfg) <= 8
     plugin.load_table(path)
     plugin.load_table(None)
@@ -50,8 +92,8 @@ def test_shipped_table_is_well_formed():
     # other families through the plan's nearest-instantiation rule
     xw = {(bm, bn, r, nw) for bm, bn, r, nw in K.XW_SHAPES}
     for row in raw.values():
-        for cfg in row.values():
-            if cfg[2] == 64:
+        for m, cfg in row.items():
+            if m != "one_launch" and cfg[2] == 64:
                 assert (cfg[0], cfg[1], cfg[4], cfg[3]) in xw, cfg
 
 

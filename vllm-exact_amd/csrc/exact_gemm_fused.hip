@@ -183,17 +183,26 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
     float amax[RPW];
 #pragma unroll
     for (int j = 0; j < RPW; ++j) amax[j] = 0.0f;
-    const int items = nrw * cpr;
-    for (int base = lane; base < items; base += 64 * PB) {
+    // this lane's items are lane + 64 t; (row jj, chunk cc) advances without a division
+    int jj = 0, cc = lane;
+    while (jj < nrw && cc >= cpr) {
+      cc -= cpr;
+      ++jj;
+    }
+    while (jj < nrw) {
       uint4 u[PB];
       int jr[PB];
 #pragma unroll
       for (int q = 0; q < PB; ++q) {
-        const int it = base + 64 * q;
         jr[q] = -1;
-        if (it < items) {
-          jr[q] = it / cpr;
-          u[q] = *reinterpret_cast<const uint4*>(p.x + (m0 + wave + NWK * jr[q]) * p.ldx + (int64_t)(it % cpr) * 8);
+        if (jj < nrw) {
+          jr[q] = jj;
+          u[q] = *reinterpret_cast<const uint4*>(p.x + (m0 + wave + NWK * jj) * p.ldx + (int64_t)cc * 8);
+          cc += 64;
+          while (jj < nrw && cc >= cpr) {
+            cc -= cpr;
+            ++jj;
+          }
         }
       }
 #pragma unroll

@@ -2,17 +2,21 @@
 
     python vllm-exact_amd/tune_table.py OUT.json [--f 14] [--shapes 6144x4096,4096x4096,...]
                                                  [--ms 1,16,64,256] [--report OUT_report.json]
+                                                 [--merge BASE.json]
 
 For each weight shape (N, K) and batch bucket M, every candidate config is run, checked
 bitwise against the first candidate's output (exact integer accumulation makes every
 tiling give the same bits; a mismatch raises), and timed by HIP-graph replay with the
-weights rotated over enough copies to stream past the 256 MB MALL. At 1-4 rows on packed
-weights with F < 15 the time is the op's: digitize inside the GEMM launch where the cfg
-allows it, digitize + GEMM otherwise. By default the weights
+weights rotated over enough copies to stream past the 256 MB MALL. By default the weights
 are packed at load time and x is digitized packed, as exactmm::linear runs them (--layout
-plain tunes the row-major kernels instead). The fastest config is
-written to {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK]}}; the report also records the
-bf16 hipBLASLt time of the same product (torch.matmul) for comparison.
+plain tunes the row-major kernels instead), and the GEMM on digitized x is timed alone.
+Up to 64 rows on packed weights with F < 15, every cfg the one-launch digitize + GEMM
+kernel takes is also timed on that path; it is chosen, and M listed in the row's
+"one_launch", when it beats digitize + the best two-launch GEMM timed together. The result
+is {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK], "one_launch": [M, ...]}}; with
+--merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept. The
+report also records the bf16 hipBLASLt time of the same product (torch.matmul) for
+comparison.
 """
 import argparse
 import json
@@ -27,6 +31,7 @@ from vllm_exact.graph_timing import rotations_for, time_graph  # noqa: E402
 
 DEFAULT_SHAPES = "6144x4096,4096x4096,24576x4096,4096x12288,151936x4096,10240x4096,12288x4096"
 SPLITS = (1, 2, 4)
+ONE_LAUNCH_TUNE_ROWS = 64  # the one-launch path is timed up to this many rows
 
 
 def candidates(M, Kd):
@@ -54,52 +59,92 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
         wds = [K.pack_digits(K.digitize(w, F)) for _ in range(rot)]
     else:
         wds = [K.digitize(w, F) for _ in range(rot)]
-    row = {}
+    row, one_rows = {}, []
     for M in ms:
         x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
         xd = K.digitize_packed(x, F) if packed else K.digitize(x, F)
-        # at 1-4 rows the op digitizes inside the GEMM launch where the cfg allows it, and
-        # launches digitize and GEMM otherwise: time that, digitize included, for every cfg
-        op_path = packed and F < 15 and M <= K.ONE_LAUNCH_MAX_ROWS
+        try_one = packed and F < 15 and M <= ONE_LAUNCH_TUNE_ROWS
 
-        def run(i, cfg):
-            if op_path:
-                try:
-                    return K.exact_linear_bf16x(x, wds[i], Kd, F, trunc, cfg=cfg)
-                except NotImplementedError:
-                    return K.exact_linear_packed(K.digitize_packed(x, F), wds[i], Kd, F, trunc, cfg=cfg)
+        def gemm(i, cfg, xd=xd):
             if packed:
                 return K.exact_linear_packed(xd, wds[i], Kd, F, trunc, cfg=cfg)
             return K.exact_linear(xd, wds[i], F, trunc, cfg=cfg)
 
-        ref, best, tried = None, None, []
-        for cfg in candidates(M, Kd):
-            try:
-                y = run(0, cfg)
-            except NotImplementedError:
-                continue
+        def two_launch(i, cfg):
+            return K.exact_linear_packed(K.digitize_packed(x, F), wds[i], Kd, F, trunc, cfg=cfg)
+
+        def one_launch(i, cfg):
+            return K.exact_linear_bf16x(x, wds[i], Kd, F, trunc, cfg=cfg)
+
+        ref, tried, tried_one = None, [], []
+
+        def check(y, cfg):
+            nonlocal ref
             if ref is None:
                 ref = y
             elif not torch.equal(y.view(torch.int32), ref.view(torch.int32)):
                 raise RuntimeError(f"config {cfg} changed the result (N={N} K={Kd} M={M})")
-            t = time_graph(lambda i, c=cfg: run(i, c), rot)
-            tried.append((t, cfg))
+
+        for cfg in candidates(M, Kd):
+            try:
+                y = gemm(0, cfg)
+            except NotImplementedError:
+                continue
+            check(y, cfg)
+            tried.append((time_graph(lambda i, c=cfg: gemm(i, c), rot), cfg))
+            if try_one:
+                try:
+                    y = one_launch(0, cfg)
+                except NotImplementedError:
+                    pass
+                else:
+                    check(y, cfg)
+                    tried_one.append((time_graph(lambda i, c=cfg: one_launch(i, c), rot), cfg))
             if len(tried) % 40 == 0:
                 print(f"  N={N} K={Kd} M={M}: {len(tried)} configs timed", file=sys.stderr, flush=True)
-            if best is None or t < best[0]:
-                best = (t, cfg)
+        best = min(tried)
+        rec = dict(N=N, K=Kd, M=M, exact_us=round(best[0], 2), cfg=list(best[1]), candidates=len(tried))
+        if tried_one:
+            # what the op would run either way: digitize + the best GEMM, or the one launch
+            t_two = time_graph(lambda i: two_launch(i, best[1]), rot)
+            best_one = min(tried_one)
+            rec.update(two_launch_op_us=round(t_two, 2), one_launch_us=round(best_one[0], 2),
+                       one_launch_cfg=list(best_one[1]), one_launch=best_one[0] < t_two)
+            if best_one[0] < t_two:
+                best = best_one
+                one_rows.append(M)
         wbs = [w.clone() for _ in range(rot)]
         t_bf16 = time_graph(lambda i: torch.matmul(x, wbs[i].T), rot)
         del wbs
         row[str(M)] = list(best[1])
-        rec = dict(N=N, K=Kd, M=M, exact_us=round(best[0], 2), bf16_hipblaslt_us=round(t_bf16, 2),
-                   cfg=list(best[1]), candidates=len(tried))
+        rec.update(bf16_hipblaslt_us=round(t_bf16, 2), chosen=list(best[1]))
         print(json.dumps(rec), flush=True)
         rec["all"] = sorted([round(t, 2), list(c)] for t, c in tried)
+        rec["all_one_launch"] = sorted([round(t, 2), list(c)] for t, c in tried_one)
         report.append(rec)
+    if packed and F < 15:
+        row["one_launch"] = one_rows
     del wds
     torch.cuda.empty_cache()
     return row
+
+
+def merge_row(old, new, ms):
+    """Row `old` with the tuned entries of `new` (at the row counts `ms`) put in. A row without
+    a "one_launch" list follows the op's default (1-4 rows); merged, it keeps that meaning for
+    the entries that were not retuned."""
+    cfgs = {m: c for m, c in old.items() if m != "one_launch"}
+    cfgs.update({m: c for m, c in new.items() if m != "one_launch"})
+    out = dict(sorted(cfgs.items(), key=lambda t: int(t[0])))
+    if "one_launch" in new:
+        if "one_launch" in old:
+            kept = [m for m in old["one_launch"] if m not in ms]
+        else:
+            kept = [int(m) for m in old if int(m) <= K.ONE_LAUNCH_MAX_ROWS and int(m) not in ms]
+        out["one_launch"] = sorted(set(kept) | set(new["one_launch"]))
+    elif "one_launch" in old:
+        out["one_launch"] = old["one_launch"]
+    return out
 
 
 def main():
@@ -109,6 +154,7 @@ def main():
     ap.add_argument("--shapes", default=DEFAULT_SHAPES)
     ap.add_argument("--ms", default="1,2,4,8,16,24,32,48,64,96,128,192,256")
     ap.add_argument("--report", default=None)
+    ap.add_argument("--merge", default=None, help="existing table whose untuned entries are kept")
     ap.add_argument("--layout", default="packed", choices=["packed", "plain"],
                     help="packed: weights packed at load (the exactmm::linear path); plain: row-major digits")
     args = ap.parse_args()
@@ -116,9 +162,11 @@ def main():
     shapes = [tuple(map(int, s.split("x"))) for s in args.shapes.split(",")]
     ms = [int(m) for m in args.ms.split(",")]
     gen = torch.Generator(device="cuda").manual_seed(0)
-    table, report = {}, []
+    table = json.loads(Path(args.merge).read_text()) if args.merge else {}
+    report = []
     for N, Kd in shapes:
-        table[f"{N},{Kd}"] = tune_shape(N, Kd, ms, F, trunc, gen, report, args.layout == "packed")
+        new = tune_shape(N, Kd, ms, F, trunc, gen, report, args.layout == "packed")
+        table[f"{N},{Kd}"] = merge_row(table.get(f"{N},{Kd}", {}), new, ms)
     Path(args.out).write_text(json.dumps(table, indent=1))
     rep = args.report or args.out.replace(".json", "_report.json")
     Path(rep).write_text(json.dumps(report, indent=1))

@@ -201,9 +201,11 @@ def exact_linear_packed(xp, wp, K, F, trunc=False, out=None, cfg=None):
     return out
 
 
-# The exactmm::linear op digitizes inside the GEMM launch (exact_linear_bf16x) up to this many
-# rows. Measured on MI355X: the one launch saves 2-6 µs per op at 1-4 rows; at 16 rows the
-# workgroups' own row pass costs what the digitize launch does, and at 64 it costs more.
+# Without a tuning-table entry that says otherwise, the exactmm::linear op digitizes inside the
+# GEMM launch (exact_linear_bf16x) up to this many rows. Measured on MI355X the one launch
+# saves 2-6 µs per op at 1-4 rows at every decode shape. Above that it depends on the shape:
+# every workgroup reads its x rows twice (row pass, then K loop), so at 16 rows it still wins
+# where K = 4096 and loses where K = 12288, and at 64 rows it loses. The tuner times both.
 ONE_LAUNCH_MAX_ROWS = 4
 
 

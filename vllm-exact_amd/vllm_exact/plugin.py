@@ -30,16 +30,25 @@ RB = 16384  # rows per block: rows are independent, so blocking bounds temporari
 WEIGHT_RB = 32768  # weight rows digitized per block at load time (plugin.py:74)
 
 
+_ONE_LAUNCH_ROWS = {}  # (N, K) -> tuned row counts whose calls digitize inside the GEMM launch
+
+
 def load_table(path):
     """Tuning table {"N,K": {"M": [BM, BN, BK, warps, stages, GM, SK(, mma)]}} (plugin.py:27-34).
-    Configs change speed only, never results."""
+    Configs change speed only, never results. A row may also hold "one_launch": [M, ...], the
+    tuned row counts at which the op digitizes inside the GEMM launch (see _one_launch)."""
     global _TABLE
+    _ONE_LAUNCH_ROWS.clear()
     if path is None:
         _TABLE = None
         return
     raw = json.loads(Path(path).read_text())
-    _TABLE = {tuple(int(v) for v in nk.split(",")): {int(m): tuple(c) for m, c in row.items()}
-              for nk, row in raw.items()}
+    _TABLE = {}
+    for nk, row in raw.items():
+        key = tuple(int(v) for v in nk.split(","))
+        _TABLE[key] = {int(m): tuple(c) for m, c in row.items() if m != "one_launch"}
+        if "one_launch" in row:
+            _ONE_LAUNCH_ROWS[key] = frozenset(int(m) for m in row["one_launch"])
 
 
 # Built-in gfx950 configs when a shape has no table entry (speed only).
@@ -62,6 +71,18 @@ def _cfg(M, N, Kd):
     return LARGE_M_CFG
 
 
+def _one_launch(M, N, Kd):
+    """Whether an (M, N, K) call takes the one-launch digitize + GEMM path: as the table row
+    that _cfg picks says when the shape's row has a "one_launch" list, else M <= 4
+    (K.ONE_LAUNCH_MAX_ROWS). Either way the bits are those of the two-launch path."""
+    if _TABLE is not None and (N, Kd) in _ONE_LAUNCH_ROWS:
+        ms = sorted(_TABLE[(N, Kd)])
+        if M > ms[-1]:
+            return False
+        return next(m for m in ms if m >= M) in _ONE_LAUNCH_ROWS[(N, Kd)]
+    return M <= K.ONE_LAUNCH_MAX_ROWS
+
+
 # cfgs the one-launch digitize + GEMM path refused (two-row tiles, split-K, other families)
 _ONE_LAUNCH_CFG = {}
 
@@ -71,8 +92,8 @@ def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: tor
                     sw: torch.Tensor) -> torch.Tensor:
     """y = x @ W^T through the exact path: reshape to 2-D, digitize x (bf16 read directly),
     exact matmul straight into an x.dtype output, in row blocks of RB (plugin.py:51-64). With
-    packed weights, 1-4 bf16 rows and a one-row-tile cfg, digitize and GEMM share one launch
-    (same bits).
+    packed weights, bf16 rows, a one-row-tile cfg and a row count the table marks (1-4 rows
+    without a mark), digitize and GEMM share one launch (same bits).
 
     Weights come either as the reference's row-major digit planes wh, wl [N, K], or packed
     at load time (wh = packed [cdiv(N,16), cdiv(K,64), 2, 1024], wl empty); N is sw's length
@@ -89,7 +110,7 @@ def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: tor
         xb = x2[i:i + RB]
         cfg = _cfg(xb.shape[0], N, Kd)
         if packed:
-            if (xb.shape[0] <= K.ONE_LAUNCH_MAX_ROWS and xb.dtype == torch.bfloat16 and F < 15
+            if (xb.dtype == torch.bfloat16 and F < 15 and _one_launch(xb.shape[0], N, Kd)
                     and _ONE_LAUNCH_CFG.get(cfg, True)):
                 # digitize inside the GEMM launch where the cfg allows it (same bits, one launch fewer)
                 try:
