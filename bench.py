@@ -171,12 +171,14 @@ def read_traffic(kernel_cfg):
 
 
 def profile_kernel(args):
-    """Launch the dominant GEMM and a plain copy of known size --steps times each (counter runs)."""
+    """Launch the dominant GEMM --steps times, its weights rotated over copies as in the timed
+    run, then a plain copy of known size --steps times (kernel-trace and counter runs)."""
     import torch
 
     from vllm_exact import _native
     from vllm_exact import kernels as K
     from vllm_exact import plugin
+    from vllm_exact.graph_timing import rotations_for
 
     _native.lib()
     dev = torch.device("cuda:0")
@@ -187,20 +189,23 @@ def profile_kernel(args):
     cfg = plugin._cfg(M, N, Kd)
     w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
     wp, _, cw, sw = plugin.pack_weight(w)
+    rot = rotations_for(2 * N * Kd)
+    wps = [wp] + [wp.clone() for _ in range(rot - 1)]
     x = torch.randn(M, Kd, device=dev, generator=gen).to(torch.bfloat16)
     xd = K.digitize_packed(x, F)
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     src = torch.randn(1 << 29, device=dev, generator=gen).to(torch.bfloat16)  # 1 GiB
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    for _ in range(args.steps):
-        K.exact_linear_packed(xd, (wp, cw, sw), Kd, F, TRUNC, out=out, cfg=cfg)
+    for i in range(args.steps):
+        K.exact_linear_packed(xd, (wps[i % rot], cw, sw), Kd, F, TRUNC, out=out, cfg=cfg)
     torch.cuda.synchronize()
     for _ in range(args.steps):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"gemm": f"M={M} {name} {N}x{Kd}", "cfg": list(cfg), "launches": args.steps,
-                      "copy_bytes": src.numel() * 2, "algorithmic_bytes": gemm_bytes(M, N, Kd)}), flush=True)
+                      "weight_copies": rot, "copy_bytes": src.numel() * 2,
+                      "algorithmic_bytes": gemm_bytes(M, N, Kd)}), flush=True)
 
 
 def profile_counters(args):
