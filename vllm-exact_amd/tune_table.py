@@ -7,15 +7,17 @@
 For each weight shape (N, K) and batch bucket M, every candidate config is run, checked
 bitwise against the first candidate's output (exact integer accumulation makes every
 tiling give the same bits; a mismatch raises), and timed by HIP-graph replay with the
-weights rotated over enough copies to stream past the 256 MB MALL. By default the weights
+weights rotated over enough copies to stream past the 256 MB MALL: a short replay of every
+candidate first, then the FINALISTS fastest in full (about 4 ms of calls per replay, 25
+replays, 10 for the big lm_heads; the median counts). By default the weights
 are packed at load time and x is digitized packed, as exactmm::linear runs them (--layout
 plain tunes the row-major kernels instead), and the GEMM on digitized x is timed alone.
 Up to 64 rows on packed weights with F < 15, every cfg the one-launch digitize + GEMM
 kernel takes is also timed on that path; it is chosen, and M listed in the row's
 "one_launch", when it beats digitize + the best two-launch GEMM timed together. The result
 is {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK], "one_launch": [M, ...]}}; with
---merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept. The
-report also records the bf16 hipBLASLt time of the same product (torch.matmul) for
+--merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept. OUT
+is rewritten after every shape. The report also records the bf16 hipBLASLt time of the same product (torch.matmul) for
 comparison.
 """
 import argparse
@@ -29,9 +31,20 @@ sys.path.insert(0, str(Path(__file__).resolve().parent))
 from vllm_exact import kernels as K  # noqa: E402
 from vllm_exact.graph_timing import rotations_for, time_graph  # noqa: E402
 
-DEFAULT_SHAPES = "6144x4096,4096x4096,24576x4096,4096x12288,151936x4096,10240x4096,12288x4096"
+# the decode sweep's qkv and lm_head, then the reference's shapes (its scripts/tune_table.py:26)
+DEFAULT_SHAPES = ("6144x4096,151936x4096,10240x4096,4096x4096,12288x4096,64x4096,24576x4096,4096x12288,"
+                  "248320x4096")
 SPLITS = (1, 2, 4)
 ONE_LAUNCH_TUNE_ROWS = 64  # the one-launch path is timed up to this many rows
+FINALISTS = 6  # candidates per path re-timed in full after the first cut
+
+
+def timing_for(M, N, Kd, rot):
+    """(calls per replay, replays) for one timing: about 4 ms of calls per replay, at least one
+    full weight rotation, and fewer replays for calls of 200 µs or more (the big lm_heads)."""
+    est_us = max(2 * N * Kd / 5e6, 6 * M * N * Kd / 2e12, 5.0)  # ~5 TB/s, ~2 POP/s
+    calls = max(rot, min(20, -(-4000 // int(est_us))))
+    return calls, (25 if est_us < 200 else 10)
 
 
 def candidates(M, Kd):
@@ -59,6 +72,7 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
         wds = [K.pack_digits(K.digitize(w, F)) for _ in range(rot)]
     else:
         wds = [K.digitize(w, F) for _ in range(rot)]
+    wbs = [w.clone() for _ in range(rot)]  # bf16 copies for the hipBLASLt comparison
     row, one_rows = {}, []
     for M in ms:
         x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
@@ -76,6 +90,13 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
         def one_launch(i, cfg):
             return K.exact_linear_bf16x(x, wds[i], Kd, F, trunc, cfg=cfg)
 
+        cpr, reps = timing_for(M, N, Kd, rot)
+
+        def timed(fn, quick=False):
+            if quick:  # a first cut over every candidate: one rotation's calls, 3 replays
+                return time_graph(fn, rot, calls_per_replay=max(rot, 2), replays=3)
+            return time_graph(fn, rot, calls_per_replay=cpr, replays=reps)
+
         ref, tried, tried_one = None, [], []
 
         def check(y, cfg):
@@ -91,7 +112,7 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
             except NotImplementedError:
                 continue
             check(y, cfg)
-            tried.append((time_graph(lambda i, c=cfg: gemm(i, c), rot), cfg))
+            tried.append((timed(lambda i, c=cfg: gemm(i, c), quick=True), cfg))
             if try_one:
                 try:
                     y = one_launch(0, cfg)
@@ -99,32 +120,34 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
                     pass
                 else:
                     check(y, cfg)
-                    tried_one.append((time_graph(lambda i, c=cfg: one_launch(i, c), rot), cfg))
+                    tried_one.append((timed(lambda i, c=cfg: one_launch(i, c), quick=True), cfg))
             if len(tried) % 40 == 0:
                 print(f"  N={N} K={Kd} M={M}: {len(tried)} configs timed", file=sys.stderr, flush=True)
+        n_cand = len(tried)
+        # the finalists of the first cut, timed in full
+        tried = sorted((timed(lambda i, c=c: gemm(i, c)), c) for _, c in sorted(tried)[:FINALISTS])
+        tried_one = sorted((timed(lambda i, c=c: one_launch(i, c)), c) for _, c in sorted(tried_one)[:FINALISTS])
         best = min(tried)
-        rec = dict(N=N, K=Kd, M=M, exact_us=round(best[0], 2), cfg=list(best[1]), candidates=len(tried))
+        rec = dict(N=N, K=Kd, M=M, exact_us=round(best[0], 2), cfg=list(best[1]), candidates=n_cand)
         if tried_one:
             # what the op would run either way: digitize + the best GEMM, or the one launch
-            t_two = time_graph(lambda i: two_launch(i, best[1]), rot)
+            t_two = timed(lambda i: two_launch(i, best[1]))
             best_one = min(tried_one)
             rec.update(two_launch_op_us=round(t_two, 2), one_launch_us=round(best_one[0], 2),
                        one_launch_cfg=list(best_one[1]), one_launch=best_one[0] < t_two)
             if best_one[0] < t_two:
                 best = best_one
                 one_rows.append(M)
-        wbs = [w.clone() for _ in range(rot)]
-        t_bf16 = time_graph(lambda i: torch.matmul(x, wbs[i].T), rot)
-        del wbs
+        t_bf16 = timed(lambda i: torch.matmul(x, wbs[i].T))
         row[str(M)] = list(best[1])
         rec.update(bf16_hipblaslt_us=round(t_bf16, 2), chosen=list(best[1]))
         print(json.dumps(rec), flush=True)
-        rec["all"] = sorted([round(t, 2), list(c)] for t, c in tried)
-        rec["all_one_launch"] = sorted([round(t, 2), list(c)] for t, c in tried_one)
+        rec["finalists"] = [[round(t, 2), list(c)] for t, c in tried]
+        rec["finalists_one_launch"] = [[round(t, 2), list(c)] for t, c in tried_one]
         report.append(rec)
     if packed and F < 15:
         row["one_launch"] = one_rows
-    del wds
+    del wds, wbs
     torch.cuda.empty_cache()
     return row
 
@@ -167,6 +190,7 @@ def main():
     for N, Kd in shapes:
         new = tune_shape(N, Kd, ms, F, trunc, gen, report, args.layout == "packed")
         table[f"{N},{Kd}"] = merge_row(table.get(f"{N},{Kd}", {}), new, ms)
+        Path(args.out).write_text(json.dumps(table, indent=1))  # after every shape
     Path(args.out).write_text(json.dumps(table, indent=1))
     rep = args.report or args.out.replace(".json", "_report.json")
     Path(rep).write_text(json.dumps(report, indent=1))
