@@ -174,6 +174,24 @@ int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh,
                      int64_t block_size, int64_t max_len, int64_t split, int64_t blk,
                      int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream);
 
+/*
+ * vxa_paged_decode for the first *n_live requests, with the count read on the device:
+ * n (>= *n_live) sizes the grid and the workspace, and the workgroups of requests at or past
+ * *n_live return before reading their length, block table, query or cache, and write nothing.
+ * Replaces the host round trip of the mixed-step path in paged_attn.py:154-159, where the
+ * number of leading decode requests is read back with .item() before the launch; here it
+ * stays on the GPU. n_live must be a device pointer (VXA_ERR_ARG when null).
+ */
+int vxa_paged_decode_prefix(const void* q, int64_t sqt, int64_t sqh,
+                            const void* k_cache, int64_t skb, int64_t skp, int64_t skh,
+                            const void* v_cache, int64_t svb, int64_t svp, int64_t svh,
+                            const int32_t* block_table, int64_t sbt, const int32_t* seq_lens,
+                            float scale, void* out, int out_dtype, int64_t sot, int64_t soh,
+                            int64_t n, const int32_t* n_live, int64_t num_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                            int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws,
+                            size_t ws_bytes, vxa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,6 +111,16 @@ def test_entry_points_validate_before_launching():
     assert call(max_len=4096) == nx.VXA_ERR_WORKSPACE
     assert call(n=0) == nx.VXA_OK
 
+    # the device-count variant: the same checks, and the count pointer is required
+    def call_prefix(n_live=fake, **over):
+        a = list(dict(args, **over).values())
+        return L.vxa_paged_decode_prefix(*a[:20], n_live, *a[20:])
+
+    assert call_prefix(n_live=None) == nx.VXA_ERR_ARG
+    assert call_prefix(D=96) == nx.VXA_ERR_UNSUPPORTED
+    assert call_prefix(max_len=4096) == nx.VXA_ERR_WORKSPACE
+    assert call_prefix(n=0) == nx.VXA_OK
+
 
 def test_fused_entry_point_validates_before_launching():
     # vxa_exact_linear_bf16x refuses what its one launch does not cover (the op then takes the

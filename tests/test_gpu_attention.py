@@ -50,6 +50,27 @@ def _check_tol_bf16(got, want):
     assert (err <= RTOL_BF16 * np.abs(want) + ATOL_F32).all(), (err - RTOL_BF16 * np.abs(want)).max()
 
 
+@pytest.mark.parametrize("L", [300, 5000])
+def test_device_count_limits_the_requests(L):
+    """paged_decode with n_live (vxa_paged_decode_prefix): the grid covers n requests, the
+    count on the GPU picks the first n_live; those rows are bitwise the plain entry point's
+    and the others are never written. L = 5000 spans several segments (merge kernel)."""
+    B, H, KV, D = 6, 8, 2, 128
+    q, kv, bt, sl = make_paged(B, L, 16, H, KV, D, seed=21)
+    q, kv, bt, sl = (t.to(DEV) for t in (q, kv, bt, sl))
+    scale = D ** -0.5
+    ref = _run(q, kv, bt, sl, scale, B, D)
+    kc, vc = kv_views(kv, D)
+    for live in (0, 3, 6):
+        out = torch.full((B, H, D), float("nan"), device=DEV)
+        P.paged_decode(q, kc, vc, bt, sl, scale, out, B, int(sl.max()),
+                       n_live=torch.tensor([live], dtype=torch.int32, device=DEV))
+        assert torch.equal(out[:live].view(torch.int32), ref[:live].view(torch.int32)), live
+        assert torch.isnan(out[live:]).all(), live
+    with pytest.raises(ValueError, match="n_live"):
+        P.paged_decode(q, kc, vc, bt, sl, scale, out, B, 0, n_live=torch.tensor([1], device=DEV))
+
+
 @pytest.mark.parametrize("B,L,BS", [(8, 300, 16), (8, 5000, 528), (4, 9000, 528), (64, 8192, 528)])
 def test_paged_attention_reference_cases(B, L, BS):
     """tests/test_gpu.py:57-78: H=16, KV=4, D=256, cache x0.5, scale 1/16."""

@@ -41,6 +41,7 @@ struct PagedParams {
   int32_t bs;        // page size (tokens per block)
   int32_t bs_shift;  // log2(bs) when bs is a power of two, else -1
   int64_t n;
+  const int32_t* n_live;  // device count of requests to compute (<= n), or null for all n
   float* mp;  // [n][H][ns]
   float* lp;  // [n][H][ns]
   float* ap;  // [n][H][ns][D]
@@ -112,6 +113,7 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
   const int64_t rem = blockIdx.x % per_seg;
   const int b = (int)(rem / p.KV);
   const int g = (int)(rem % p.KV);
+  if (p.n_live != nullptr && b >= *p.n_live) return;  // not a live request: nothing read or written
 
   const int L = p.sl[b];
   const int start = s * p.split;
@@ -290,6 +292,7 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
   const int64_t bh = blockIdx.x;
   const int b = (int)(bh / p.H);
   const int head = (int)(bh % p.H);
+  if (p.n_live != nullptr && b >= *p.n_live) return;
   const int L = p.sl[b];
   const int nsb = min((L + p.split - 1) / p.split, p.ns);
   if (nsb == 1) return;  // written by the partial kernel
@@ -370,13 +373,15 @@ extern "C" int vxa_paged_decode_workspace(int64_t n, int64_t num_heads, int64_t 
   return VXA_OK;
 }
 
-extern "C" int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh, const void* k_cache, int64_t skb,
-                                int64_t skp, int64_t skh, const void* v_cache, int64_t svb, int64_t svp,
-                                int64_t svh, const int32_t* block_table, int64_t sbt, const int32_t* seq_lens,
-                                float scale, void* out, int out_dtype, int64_t sot, int64_t soh, int64_t n,
-                                int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-                                int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws,
-                                size_t ws_bytes, vxa_stream_t stream) {
+namespace {
+
+int paged_decode_impl(const void* q, int64_t sqt, int64_t sqh, const void* k_cache, int64_t skb, int64_t skp,
+                      int64_t skh, const void* v_cache, int64_t svb, int64_t svp, int64_t svh,
+                      const int32_t* block_table, int64_t sbt, const int32_t* seq_lens, float scale, void* out,
+                      int out_dtype, int64_t sot, int64_t soh, int64_t n, const int32_t* n_live,
+                      int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                      int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws, size_t ws_bytes,
+                      vxa_stream_t stream) {
   if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || split <= 0)
     return VXA_ERR_ARG;
   if (out_dtype != VXA_F32 && out_dtype != VXA_BF16 && out_dtype != VXA_F16) return VXA_ERR_ARG;
@@ -422,6 +427,7 @@ extern "C" int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh, const v
     pp.bs_shift = sh;
   }
   pp.n = n;
+  pp.n_live = n_live;
   float* wsf = reinterpret_cast<float*>(ws);
   const int64_t nhs = n * num_heads * ns;
   pp.mp = ns > 1 ? wsf : nullptr;
@@ -451,4 +457,32 @@ extern "C" int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh, const v
     if (hipGetLastError() != hipSuccess) return VXA_ERR_LAUNCH;
   }
   return VXA_OK;
+}
+
+}  // namespace
+
+extern "C" int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh, const void* k_cache, int64_t skb,
+                                int64_t skp, int64_t skh, const void* v_cache, int64_t svb, int64_t svp,
+                                int64_t svh, const int32_t* block_table, int64_t sbt, const int32_t* seq_lens,
+                                float scale, void* out, int out_dtype, int64_t sot, int64_t soh, int64_t n,
+                                int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                                int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws,
+                                size_t ws_bytes, vxa_stream_t stream) {
+  return paged_decode_impl(q, sqt, sqh, k_cache, skb, skp, skh, v_cache, svb, svp, svh, block_table, sbt, seq_lens,
+                           scale, out, out_dtype, sot, soh, n, nullptr, num_heads, num_kv_heads, head_dim,
+                           block_size, max_len, split, blk, waves, ws, ws_bytes, stream);
+}
+
+extern "C" int vxa_paged_decode_prefix(const void* q, int64_t sqt, int64_t sqh, const void* k_cache, int64_t skb,
+                                       int64_t skp, int64_t skh, const void* v_cache, int64_t svb, int64_t svp,
+                                       int64_t svh, const int32_t* block_table, int64_t sbt,
+                                       const int32_t* seq_lens, float scale, void* out, int out_dtype,
+                                       int64_t sot, int64_t soh, int64_t n, const int32_t* n_live,
+                                       int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                       int64_t block_size, int64_t max_len, int64_t split, int64_t blk,
+                                       int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream) {
+  if (n_live == nullptr) return VXA_ERR_ARG;
+  return paged_decode_impl(q, sqt, sqh, k_cache, skb, skp, skh, v_cache, svb, svp, svh, block_table, sbt, seq_lens,
+                           scale, out, out_dtype, sot, soh, n, n_live, num_heads, num_kv_heads, head_dim,
+                           block_size, max_len, split, blk, waves, ws, ws_bytes, stream);
 }

@@ -10,8 +10,9 @@ Usage (enable() must be called before importing vllm), as in the reference (__in
 enable() turns on vLLM's batch-invariant mode with the engine core in-process, bypasses
 vLLM's GDN batch-invariance check, registers quantization="exact_int8" (every linear layer,
 lm_head by default, through the gfx950 exact matmul), returns the LLM keyword arguments
-(no chunked prompts, Triton GDN prefill, FLASH_ATTN backend, no prefix caching), and
-patches decode attention onto the fixed-order paged kernel.
+(no chunked prompts, Triton GDN prefill, the FLASH_ATTN backend unless another is named, no
+prefix caching), and patches that backend's decode attention onto the fixed-order paged
+kernel.
 """
 import os
 import sys
@@ -23,7 +24,13 @@ _ENABLED = False
 TABLES = {"mi355x": Path(__file__).with_name("cfg_table_mi355x_F14.json")}
 
 
-def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x", max_num_batched_tokens=131072):
+def _attention_backends():
+    from . import paged_attn
+    return paged_attn.BACKENDS
+
+
+def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x", max_num_batched_tokens=131072,
+           attention_backend="FLASH_ATTN"):
     """Return keyword arguments for vllm.LLM(...) (reference __init__.py:32-68).
 
     max_model_len: the value passed to LLM (fixes the attention kernel's segment count).
@@ -31,12 +38,16 @@ def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x"
     cfg_table: "mi355x", a path to a table, or None (built-in configs). Tables change speed
       only, never results.
     max_num_batched_tokens: must exceed every prompt length (prompts are never chunked).
+    attention_backend: the vLLM backend whose decode path is replaced (paged_attn.BACKENDS;
+      the reference always uses FLASH_ATTN). vLLM is asked for the same backend.
     """
     global _ENABLED
     if _ENABLED:
         raise RuntimeError("vllm_exact.enable() can only be called once")
     if "vllm" in sys.modules:
         raise RuntimeError("vllm_exact.enable() must be called before importing vllm")
+    if attention and attention_backend not in _attention_backends():
+        raise ValueError(f"attention_backend must be one of {sorted(_attention_backends())}")
     if cfg_table in ("h200", "b300"):
         raise ValueError(f"the {cfg_table} table describes another GPU; use 'mi355x', a path, or None")
     os.environ["VLLM_BATCH_INVARIANT"] = "1"
@@ -58,7 +69,7 @@ def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x"
     if attention:
         from . import paged_attn
         paged_attn.MAX_LEN = max_model_len
-        paged_attn.install()
-        kw["attention_config"] = {"backend": "FLASH_ATTN"}
+        paged_attn.install(attention_backend)
+        kw["attention_config"] = {"backend": attention_backend}
     _ENABLED = True
     return kw

@@ -38,6 +38,7 @@ EXPORTED = (
     "vxa_exact_linear_bf16x",
     "vxa_paged_decode_workspace",
     "vxa_paged_decode",
+    "vxa_paged_decode_prefix",
 )
 
 _i64, _i32, _int, _vp, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
@@ -72,6 +73,11 @@ _SIGNATURES = {
         _int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp,
          _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp],
+    ),
+    "vxa_paged_decode_prefix": (
+        _int,
+        [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp,
+         _int, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _sz, _vp],
     ),
 }
 
