@@ -146,6 +146,27 @@ def test_op_with_packed_weights_matches_oracle(shape):
             plugin.load_table(None)
 
 
+def test_layer_digitize_and_weight_release():
+    """process_weights_after_loading's packing of a layer (plugin.py:72-79): the op on the
+    layer's buffers gives the oracle's bits, and releasing the bf16 weight afterwards
+    (enable(release_weights=True)) frees its memory and changes no bit."""
+    g = torch.Generator().manual_seed(13)
+    w = (torch.randn(160, 512, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(3, 512, generator=g).to(torch.bfloat16)
+    kept, freed = torch.nn.Linear(512, 160, bias=False), torch.nn.Linear(512, 160, bias=False)
+    for layer in (kept, freed):
+        layer.weight.data = w.to(DEV)
+    plugin._digitize_layer(kept)
+    plugin._digitize_layer(freed, release=True)
+    assert kept.weight.numel() == 160 * 512
+    assert freed.weight.numel() == 0 and freed.weight.dtype == torch.bfloat16 and freed.weight.is_cuda
+    ys = [plugin._apply(layer, x.to(DEV), None) for layer in (kept, freed)]
+    assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
+    ref = oracle.exact_linear_c(oracle.digitize_c(x.float().numpy(), plugin.F),
+                                oracle.digitize_c(w.float().numpy(), plugin.F), plugin.F, plugin.TRUNC)
+    assert np.array_equal(ys[1].cpu().view(torch.int16).numpy().view(np.uint16), oracle.bf16_rne_c(ref).reshape(3, 160))
+
+
 def test_op_row_blocks_and_input_layouts():
     """exactmm::linear cuts M into RB-row blocks (plugin.py:60-63), each with the config of its
     own size; rows are independent, so any blocking, a 3-D input and a transposed (strided)

@@ -30,7 +30,7 @@ def _attention_backends():
 
 
 def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x", max_num_batched_tokens=131072,
-           attention_backend="FLASH_ATTN"):
+           attention_backend="FLASH_ATTN", release_weights=False):
     """Return keyword arguments for vllm.LLM(...) (reference __init__.py:32-68).
 
     max_model_len: the value passed to LLM (fixes the attention kernel's segment count).
@@ -40,6 +40,9 @@ def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x"
     max_num_batched_tokens: must exceed every prompt length (prompts are never chunked).
     attention_backend: the vLLM backend whose decode path is replaced (paged_attn.BACKENDS;
       the reference always uses FLASH_ATTN). vLLM is asked for the same backend.
+    release_weights: free each linear layer's bf16 weight once its digits are packed (the
+      lm_head's is kept). The reference keeps both copies; this halves the weight memory but
+      breaks code that reads a linear layer's .weight after loading.
     """
     global _ENABLED
     if _ENABLED:
@@ -59,6 +62,7 @@ def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x"
     plugin.F = f
     plugin.TRUNC = f == 14
     plugin.LMHEAD = lm_head
+    plugin.RELEASE_WEIGHTS = bool(release_weights)
     plugin.load_table(TABLES.get(cfg_table, cfg_table) if cfg_table else None)
 
     from vllm.v1.attention.backends.gdn_attn import GDNAttentionBackend

@@ -25,6 +25,7 @@ except ImportError:
 F = 14
 TRUNC = True
 LMHEAD = True
+RELEASE_WEIGHTS = False  # free each linear layer's bf16 weight once its digits are packed
 _TABLE = None
 RB = 16384  # rows per block: rows are independent, so blocking bounds temporaries without changing bits
 WEIGHT_RB = 32768  # weight rows digitized per block at load time (plugin.py:74)
@@ -153,12 +154,17 @@ def pack_weight(w):
     return packed, torch.empty(0, dtype=torch.int8, device=w.device), cw, sw
 
 
-def _digitize_layer(layer):
+def _digitize_layer(layer, release=False):
+    """Register the packed digits of layer.weight as buffers (plugin.py:72-79). With release,
+    the bf16 weight's memory is freed afterwards: the Parameter stays (same dtype and device,
+    no elements), so nothing that only checks for it breaks, but the op never reads it."""
     ph, pl, cs, sh = pack_weight(layer.weight.data)
     layer.register_buffer("ex_wh", ph, persistent=False)
     layer.register_buffer("ex_wl", pl, persistent=False)
     layer.register_buffer("ex_cw", cs, persistent=False)
     layer.register_buffer("ex_sw", sh, persistent=False)
+    if release:
+        layer.weight.data = layer.weight.data.new_empty(0)
 
 
 def _apply(layer, x, bias):
@@ -170,13 +176,14 @@ if HAVE_VLLM:
 
     class ExactLinearMethod(UnquantizedLinearMethod):
         def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
-            _digitize_layer(layer)
+            _digitize_layer(layer, release=RELEASE_WEIGHTS)
 
         def apply(self, layer, x, bias=None):
             return _apply(layer, x, bias)
 
     class ExactLMHeadMethod(UnquantizedEmbeddingMethod):
-        """lm_head through the exact linear layer; the embedding lookup is unchanged."""
+        """lm_head through the exact linear layer; the embedding lookup is unchanged. Its bf16
+        weight is always kept: a tied lm_head shares it with the embedding."""
 
         def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
             _digitize_layer(layer)
