@@ -69,7 +69,7 @@ FUSED_CFGS = tuple((16, 16 * nt, 128, nwk, c, 8, 1) for mt, nt, c, nwk in K.SMAL
 
 
 @pytest.mark.parametrize("F,tr", [(14, True), (14, False), (12, True)])
-@pytest.mark.parametrize("M,N,Kd", [(1, 64, 4096), (2, 200, 1000), (3, 96, 4104), (4, 48, 64), (4, 16, 12288),
+@pytest.mark.parametrize("M,N,Kd", [(1, 64, 4096), (2, 200, 1000), (3, 96, 4104), (4, 48, 64), (4, 16, 12288), (2, 5000, 4096),
                                     (1, 130, 40), (16, 64, 4096), (37, 80, 1000), (64, 48, 12288), (20, 32, 8)])
 def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
     """exact_linear_bf16x (x digitized inside the GEMM launch, each workgroup its own 16 rows)

@@ -306,10 +306,220 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
   }
 }
 
+// The same product with x read once, into registers, in the MFMA operand layout: lane
+// (r16, kq) of wave w holds its row's 16 columns of every K step w + NWK * i, i < XS (8 VGPRs
+// a step). The row absmax comes from those registers (the 4 lanes of a row in a wave, then
+// the waves through LDS), and the K loop converts them, so x costs one read and no second
+// round trip before the first MFMA. The first round's weights are issued right after x and
+// arrive during the absmax; each later round's weights are issued before the MFMAs of the
+// round before it. Needs cdiv(KT, NWK) <= XS (the launcher picks XS).
+template <int NT, int NWK, int C, bool TRUNC, int XS>
+__global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams p) {
+  static_assert(XS % C == 0, "rounds of C steps");
+  constexpr int BN = 16 * NT;
+  constexpr int NR = XS / C;  // rounds
+  __shared__ unsigned long long red[16 * BN];
+  __shared__ float s_max[NWK][16];
+  __shared__ float s_scale[16];
+  __shared__ int32_t s_sh[16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int nthr = 64 * NWK;
+  const int64_t nbn = cdiv<int64_t>(p.N, BN);
+  const int64_t bn = blockIdx.x % nbn;
+  const int64_t m0 = (int64_t)(blockIdx.x / nbn) * 16;
+  const int64_t n0 = bn * BN;
+  const int mrows = (int)min<int64_t>(16, p.M - m0);
+  const int64_t nsteps = p.KT;
+
+  for (int i = threadIdx.x; i < 16 * BN; i += nthr) red[i] = 0ull;
+
+  const bool row_ok = r16 < mrows;
+  const uint16_t* xrow = p.x + (m0 + (row_ok ? r16 : 0)) * p.ldx + kq * 16;
+  const int8_t* whp[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int64_t tile = min(bn * NT + nt, cdiv<int64_t>(p.N, 16) - 1);
+    whp[nt] = p.wp + tile * p.KT * 2048 + lane * 16;
+  }
+
+  // 1. x of this lane's steps, bf16 pairs as loaded (zeros past K and for rows past M).
+  uint32_t xw[XS][8];
+#pragma unroll
+  for (int i = 0; i < XS; ++i) {
+    const int64_t s = wave + (int64_t)NWK * i;
+    const int64_t c0 = s * 64 + kq * 16;
+    if (row_ok && s < nsteps && c0 + 16 <= p.K) {
+      const uint4 a = *reinterpret_cast<const uint4*>(xrow + s * 64);
+      const uint4 b = *reinterpret_cast<const uint4*>(xrow + s * 64 + 8);
+      xw[i][0] = a.x; xw[i][1] = a.y; xw[i][2] = a.z; xw[i][3] = a.w;
+      xw[i][4] = b.x; xw[i][5] = b.y; xw[i][6] = b.z; xw[i][7] = b.w;
+    } else if (row_ok && s < nsteps && c0 < p.K) {  // the chunk K ends in
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = c0 + 2 * e < p.K ? xrow[s * 64 + 2 * e] : 0u;
+        const uint32_t hi = c0 + 2 * e + 1 < p.K ? xrow[s * 64 + 2 * e + 1] : 0u;
+        xw[i][e] = lo | (hi << 16);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xw[i][e] = 0u;
+    }
+  }
+
+  // 2. Weights, double-buffered by round; round 0 is issued behind x.
+  v4i wh[2][C][NT], wl[2][C][NT];
+  auto load_round = [&](int r, int buf) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t s = wave + (int64_t)NWK * (r * C + c);
+      if (s < nsteps) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          wh[buf][c][nt] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(whp[nt] + s * 2048));
+          wl[buf][c][nt] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(whp[nt] + s * 2048 + 1024));
+        }
+      }
+    }
+  };
+  load_round(0, 0);
+
+  // 3. Row absmax over all of K: this lane's values, the row's 4 lanes in the wave, the waves.
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < XS; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      m = fmaxf(m, fabsf(__uint_as_float(xw[i][e] << 16)));
+      m = fmaxf(m, fabsf(__uint_as_float(xw[i][e] & 0xFFFF0000u)));
+    }
+  m = fmaxf(m, shfl_xor_f32(m, 16));
+  m = fmaxf(m, shfl_xor_f32(m, 32));
+  if (kq == 0) s_max[wave][r16] = m;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWK; ++w) a = fmaxf(a, s_max[w][threadIdx.x]);
+    int sh;
+    s_scale[threadIdx.x] = digit_scale(a, p.F, sh);
+    s_sh[threadIdx.x] = sh;
+  }
+  __syncthreads();
+  const float scale = s_scale[r16];  // rows past M hold zeros: any scale gives zero digits
+
+  // 4. K loop.
+  constexpr bool kSplitMd = NT <= 2;
+  v4i hh[NT], md[NT], mx[NT], ll[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    hh[nt] = v4i{0, 0, 0, 0};
+    md[nt] = v4i{0, 0, 0, 0};
+    mx[nt] = v4i{0, 0, 0, 0};
+    ll[nt] = v4i{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (wave + (int64_t)NWK * r * C >= nsteps) break;  // this wave has no steps left
+    if (r + 1 < NR) load_round(r + 1, (r + 1) & 1);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int i = r * C + c;
+      if (wave + (int64_t)NWK * i < nsteps) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t h4 = 0, l4 = 0;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const uint32_t w = xw[i][(4 * q + b) >> 1];
+            const float v = __uint_as_float(((4 * q + b) & 1) ? (w & 0xFFFF0000u) : (w << 16));
+            int32_t hd, ld;
+            digits_balanced(v, scale, hd, ld);
+            h4 |= ((uint32_t)hd & 255u) << (8 * b);
+            l4 |= ((uint32_t)ld & 255u) << (8 * b);
+          }
+          hw[q] = h4;
+          lw[q] = l4;
+        }
+        const v4i ah = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+        const v4i al = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+        const int buf = r & 1;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) hh[nt] = mfma_i8(ah, wh[buf][c][nt], hh[nt]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) md[nt] = mfma_i8(ah, wl[buf][c][nt], md[nt]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          if constexpr (kSplitMd) mx[nt] = mfma_i8(al, wh[buf][c][nt], mx[nt]);
+          else md[nt] = mfma_i8(al, wh[buf][c][nt], md[nt]);
+        }
+        if constexpr (!TRUNC) {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) ll[nt] = mfma_i8(al, wl[buf][c][nt], ll[nt]);
+        }
+      }
+    }
+  }
+
+  // 5. Wave partials meet in LDS (exact int64 adds), then the epilogue.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int64_t cross = (int64_t)md[nt][r];
+      if constexpr (kSplitMd) cross += (int64_t)mx[nt][r];
+      int64_t tot = ((int64_t)hh[nt][r] << 16) + (cross << 8);
+      if constexpr (!TRUNC) tot += (int64_t)ll[nt][r];
+      const int mr = kq * 4 + r;
+      if (mr < mrows) atomicAdd(&red[mr * BN + nt * 16 + r16], (unsigned long long)tot);
+    }
+  __syncthreads();
+  for (int i = threadIdx.x; i < mrows * BN; i += nthr) {
+    const int mr = i / BN;
+    const int64_t n = n0 + i % BN;
+    if (n < p.N)
+      store_f32_as(p.out, p.out_dtype, (m0 + mr) * p.ldo + n, exact_epilogue((int64_t)red[i], s_sh[mr], p.sw[n]));
+  }
+}
+
+// Instantiations of the x-in-registers kernel that compile without scratch (gfx950 -O3):
+// 4 steps a wave with at most 8 waves (at most 212 VGPRs of their 256), or with 16 waves and
+// one column tile (at most 120 of their 128); 8 steps with at most 8 waves and NT * C <= 2
+// (at most 245). Other shapes and longer K take the row-pass kernel above.
+template <int NT, int NWK, int C, int XS>
+constexpr bool xreg_fits() {
+  return (XS == 4 && (NWK <= 8 || NT == 1)) || (XS == 8 && NWK <= 8 && NT * C <= 2);
+}
+
+// Compute units of the current device (cached per device; 0 when the query fails).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 template <int NT, int NWK, int C, bool TRUNC>
 hipError_t launch(const FusedParams& fp, hipStream_t st) {
   const int64_t blocks = cdiv<int64_t>(fp.M, 16) * cdiv<int64_t>(fp.N, 16 * NT);
   if (blocks > 0x7FFFFFFFLL) return hipErrorInvalidConfiguration;
+  // x in registers when this wave's steps fit an instantiated XS and the grid is at most one
+  // workgroup per CU. Its registers (100-250 VGPRs) leave room for one workgroup a CU; with
+  // more workgroups than CUs the row-pass kernel (about 75 VGPRs) runs several per CU, which
+  // hides more latency than the saved x read gains (measured on gate_up and the lm_head).
+  const int64_t per_wave = blocks <= device_cus() ? cdiv<int64_t>(fp.KT, NWK) : INT64_MAX;
+#define VXA_XREG(XS_)                                                                                             if constexpr (XS_ % C == 0 && xreg_fits<NT, NWK, C, XS_>()) {                                                  if (per_wave <= XS_) {                                                                                            hipLaunchKernelGGL((exact_fused_xreg_kernel<NT, NWK, C, TRUNC, XS_>), dim3((unsigned)blocks), dim3(64 * NWK),                          0, st, fp);                                                                                  return hipGetLastError();                                                                                     }                                                                                                             }
+  VXA_XREG(4) VXA_XREG(8)
+#undef VXA_XREG
   if (fp.M <= 4)
     hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, true>), dim3((unsigned)blocks), dim3(64 * NWK), 0, st,
                        fp);
