@@ -67,6 +67,13 @@ def test_device_count_limits_the_requests(L):
                        n_live=torch.tensor([live], dtype=torch.int32, device=DEV))
         assert torch.equal(out[:live].view(torch.int32), ref[:live].view(torch.int32)), live
         assert torch.isnan(out[live:]).all(), live
+    # the count as install() makes it on the GPU: 3 single-token requests, then a prefill
+    qsl = torch.tensor([0, 1, 2, 3, 40, 41, 42], dtype=torch.int32, device=DEV)
+    n_live = P.leading_decodes(qsl)
+    assert n_live.is_cuda and n_live.dtype == torch.int32 and int(n_live) == 3
+    out = torch.full((B, H, D), float("nan"), device=DEV)
+    P.paged_decode(q, kc, vc, bt, sl, scale, out, B, int(sl.max()), n_live=n_live)
+    assert torch.equal(out[:3].view(torch.int32), ref[:3].view(torch.int32)) and torch.isnan(out[3:]).all()
     with pytest.raises(ValueError, match="n_live"):
         P.paged_decode(q, kc, vc, bt, sl, scale, out, B, 0, n_live=torch.tensor([1], device=DEV))
 
