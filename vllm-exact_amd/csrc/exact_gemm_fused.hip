@@ -412,7 +412,7 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
   const float scale = s_scale[r16];  // rows past M hold zeros: any scale gives zero digits
 
   // 4. K loop.
-  constexpr bool kSplitMd = NT <= 2;
+  constexpr bool kSplitMd = NT == 1 || (NT == 2 && NWK < 16);  // NT = 2 with 16 waves: one cross accumulator (128 VGPRs)
   v4i hh[NT], md[NT], mx[NT], ll[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -488,11 +488,12 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
 
 // Instantiations of the x-in-registers kernel that compile without scratch (gfx950 -O3):
 // 4 steps a wave with at most 8 waves (at most 212 VGPRs of their 256), or with 16 waves and
-// one column tile (at most 120 of their 128); 8 steps with at most 8 waves and NT * C <= 2
-// (at most 245). Other shapes and longer K take the row-pass kernel above.
-template <int NT, int NWK, int C, int XS>
+// one column tile, or two with 3 dots (at most 127 of their 128); 8 steps with at most 8
+// waves and NT * C <= 2 (at most 245). Other shapes and longer K take the row-pass kernel.
+template <int NT, int NWK, int C, int XS, bool TRUNC>
 constexpr bool xreg_fits() {
-  return (XS == 4 && (NWK <= 8 || NT == 1)) || (XS == 8 && NWK <= 8 && NT * C <= 2);
+  if (XS == 4) return NWK <= 8 || NT == 1 || (NT == 2 && C == 1 && TRUNC);
+  return XS == 8 && NWK <= 8 && NT * C <= 2;
 }
 
 // Compute units of the current device (cached per device; 0 when the query fails).
@@ -517,7 +518,7 @@ hipError_t launch(const FusedParams& fp, hipStream_t st) {
   // more workgroups than CUs the row-pass kernel (about 75 VGPRs) runs several per CU, which
   // hides more latency than the saved x read gains (measured on gate_up and the lm_head).
   const int64_t per_wave = blocks <= device_cus() ? cdiv<int64_t>(fp.KT, NWK) : INT64_MAX;
-#define VXA_XREG(XS_)                                                                                             if constexpr (XS_ % C == 0 && xreg_fits<NT, NWK, C, XS_>()) {                                                  if (per_wave <= XS_) {                                                                                            hipLaunchKernelGGL((exact_fused_xreg_kernel<NT, NWK, C, TRUNC, XS_>), dim3((unsigned)blocks), dim3(64 * NWK),                          0, st, fp);                                                                                  return hipGetLastError();                                                                                     }                                                                                                             }
+#define VXA_XREG(XS_)                                                                                             if constexpr (XS_ % C == 0 && xreg_fits<NT, NWK, C, XS_, TRUNC>()) {                                                  if (per_wave <= XS_) {                                                                                            hipLaunchKernelGGL((exact_fused_xreg_kernel<NT, NWK, C, TRUNC, XS_>), dim3((unsigned)blocks), dim3(64 * NWK),                          0, st, fp);                                                                                  return hipGetLastError();                                                                                     }                                                                                                             }
   VXA_XREG(4) VXA_XREG(8)
 #undef VXA_XREG
   if (fp.M <= 4)
