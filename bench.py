@@ -378,7 +378,7 @@ def main():
             t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
             # the GEMM kernel the op runs: where the table marks the row count, the one-launch
             # digitize + GEMM kernel (x read as bf16), otherwise the GEMM on digits digitized beforehand
-            one_launch = F < 15 and plugin._one_launch(M, N, Kd)
+            one_launch = plugin._one_launch(M, N, Kd)
             if one_launch:
                 try:
                     K.exact_linear_bf16x(x, (wc[0][0], wc[0][2], wc[0][3]), Kd, F, TRUNC, cfg=cfg)

@@ -125,18 +125,20 @@ int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, const int32_t* 
  * Digitize x and run vxa_exact_linear_packed in one launch: the same bits as
  * vxa_digitize_packed followed by vxa_exact_linear_packed.
  *   x    bf16 [m, k], row stride ldx elements
- *   wp, sw  packed weight digits and weight shifts (as vxa_exact_linear_packed); f <= 14
+ *   wp, cw, sw  packed weight digits, digit sums and shifts (as vxa_exact_linear_packed); cw
+ *           is read for f = 15 only (may be null otherwise)
  *   cfg  a small-M config with one-row tiles (BM <= 16) and SK = 1; k <= 32768, so that the
  *        plan keeps one K split (int32 digit sums stay exact)
  * Each workgroup digitizes its own 16 rows of x (row absmax over k, then the digits in
- * registers). Returns VXA_ERR_UNSUPPORTED for f = 15, another cfg family, a plan with more
- * than one K split, or x rows that are not 16-byte aligned: the caller then takes the
- * two-launch path. No reference counterpart:
+ * registers). Returns VXA_ERR_UNSUPPORTED for another cfg family, a plan with more than one
+ * K split, x rows that are not 16-byte aligned, or f = 15 where its x-in-registers kernel
+ * does not apply (more workgroups than CUs, a K longer than its registers hold, 3 dots): the
+ * caller then takes the two-launch path. No reference counterpart:
  * the reference digitizes x in a launch of its own (plugin.py:62-64); this entry point serves
  * the exactmm::linear op at decode sizes, where that launch is a quarter of the op.
  */
-int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw,
-                           void* out, int out_dtype, int64_t ldo,
+int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* wp, const int32_t* cw,
+                           const int32_t* sw, void* out, int out_dtype, int64_t ldo,
                            int64_t m, int64_t n, int64_t k, int f, int trunc,
                            const int32_t* cfg, int cfg_len, vxa_stream_t stream);
 

@@ -129,10 +129,12 @@ def test_fused_entry_point_validates_before_launching():
     fake = 16
     sm, sm_n = nx.cfg_array((16, 32, 128, 8, 1, 8, 1))
 
-    def call(m=1, n=4096, k=4096, f=14, cfg=(sm, sm_n), x=fake, ldx=4096, od=nx.VXA_BF16, ldo=4096, w=fake):
-        return L.vxa_exact_linear_bf16x(x, ldx, w, fake, fake, od, ldo, m, n, k, f, 1, cfg[0], cfg[1], None)
+    def call(m=1, n=4096, k=4096, f=14, cfg=(sm, sm_n), x=fake, ldx=4096, od=nx.VXA_BF16, ldo=4096, w=fake,
+             cw=fake, trunc=1):
+        return L.vxa_exact_linear_bf16x(x, ldx, w, cw, fake, fake, od, ldo, m, n, k, f, trunc, cfg[0], cfg[1], None)
 
-    assert call(f=15) == nx.VXA_ERR_UNSUPPORTED  # offset digits need a row sum first
+    assert call(f=15) == nx.VXA_ERR_UNSUPPORTED  # offset digits run 4 dots in one launch, not 3
+    assert call(f=15, trunc=0, cw=None) == nx.VXA_ERR_ARG  # their epilogue needs the weight digit sums
     assert call(cfg=nx.cfg_array((64, 96, 64, 6, 6, 8, 1))) == nx.VXA_ERR_UNSUPPORTED  # not a small-M cfg
     assert call(cfg=nx.cfg_array((32, 32, 128, 8, 1, 8, 1))) == nx.VXA_ERR_UNSUPPORTED  # two row tiles
     assert call(cfg=nx.cfg_array((16, 32, 128, 8, 1, 8, 2))) == nx.VXA_ERR_UNSUPPORTED  # split-K

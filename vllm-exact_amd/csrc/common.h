@@ -66,6 +66,14 @@ __device__ inline void digits_balanced(float v, float scale, int32_t& hd, int32_
   hd = (int32_t)(uq - (uint32_t)ld) >> 8;
 }
 
+// Offset digits (F == 15, kernels.py:31-34) of q = trunc(v * scale): q = 256 h + l + 128 with
+// l in [-128, 127], in 32-bit wrap-around arithmetic.
+__device__ inline void digits_offset(float v, float scale, int32_t& hd, int32_t& ld) {
+  const uint32_t uq = (uint32_t)(int32_t)(v * scale);  // truncation toward zero
+  ld = (int32_t)(uq & 255u) - 128;
+  hd = (int32_t)(uq - (uint32_t)ld - 128u) >> 8;
+}
+
 // Workgroups are handed to the 8 XCDs round-robin (linear id % 8), and each XCD has its own
 // L2. This bijection gives XCD x the logical ids [x*base + min(x, rem), ...) in dispatch
 // order, so neighbouring logical tiles (which share an operand tile) run on one XCD at about

@@ -147,9 +147,7 @@ __global__ __launch_bounds__(kMaxThreads) void digitize_fast_kernel(const void* 
       int32_t hd = 0, ld = 0;
       if (c * 16 + j < K) {
         if constexpr (OFFSET) {
-          const uint32_t uq = (uint32_t)(int32_t)(v[i][j] * scale);  // truncation toward zero
-          ld = (int32_t)(uq & 255u) - 128;
-          hd = (int32_t)(uq - (uint32_t)ld - 128u) >> 8;
+          digits_offset(v[i][j], scale, hd, ld);
           csum += (uint32_t)(256 * hd + ld);
         } else {
           digits_balanced(v[i][j], scale, hd, ld);

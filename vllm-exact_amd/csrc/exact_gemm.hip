@@ -221,23 +221,23 @@ extern "C" int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, cons
   return run_exact(pl, ep, trunc, true, true, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw, void* out,
-                                      int out_dtype, int64_t ldo, int64_t m, int64_t n, int64_t k, int f, int trunc,
-                                      const int32_t* cfg, int cfg_len, vxa_stream_t stream) {
+extern "C" int vxa_exact_linear_bf16x(const void* x, int64_t ldx, const int8_t* wp, const int32_t* cw,
+                                      const int32_t* sw, void* out, int out_dtype, int64_t ldo, int64_t m, int64_t n,
+                                      int64_t k, int f, int trunc, const int32_t* cfg, int cfg_len,
+                                      vxa_stream_t stream) {
   if (m < 0 || n < 0 || k < 0 || f < 1 || f > 15) return VXA_ERR_ARG;
   if (out_dtype != VXA_F32 && out_dtype != VXA_BF16 && out_dtype != VXA_F16) return VXA_ERR_ARG;
-  if (f == 15) return VXA_ERR_UNSUPPORTED;  // offset digits need a row sum first
   ExactPlan pl;
   const int rc = make_plan(cdiv<int64_t>(k, 64) * 64, cfg, cfg_len, &pl);
   if (rc != VXA_OK) return rc;
   if (pl.family != kFamilySmall || pl.mt != 1 || pl.sk != 1) return VXA_ERR_UNSUPPORTED;
   if (m == 0 || n == 0) return VXA_OK;
   if (k == 0) return VXA_ERR_UNSUPPORTED;  // K = 0 has no packed form
-  if (!x || !wp || !sw || !out || ldo < n || ldx < k) return VXA_ERR_ARG;
+  if (!x || !wp || !sw || !out || ldo < n || ldx < k || (f == 15 && !cw)) return VXA_ERR_ARG;
   if ((uintptr_t)wp % 16) return VXA_ERR_ARG;
   // x rows are read 16 bytes at a time
   if ((uintptr_t)x % 16 || ldx % 8) return VXA_ERR_UNSUPPORTED;
-  const hipError_t err = launch_exact_fused(pl, x, ldx, wp, sw, out, out_dtype, ldo, m, n, k, f, trunc != 0,
+  const hipError_t err = launch_exact_fused(pl, x, ldx, wp, cw, sw, out, out_dtype, ldo, m, n, k, f, trunc != 0,
                                             reinterpret_cast<hipStream_t>(stream));
   if (err == hipErrorInvalidValue) return VXA_ERR_UNSUPPORTED;
   return err == hipSuccess ? VXA_OK : VXA_ERR_LAUNCH;

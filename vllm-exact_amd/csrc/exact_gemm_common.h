@@ -81,11 +81,12 @@ hipError_t launch_exact_lds(const ExactPlan& pl, const ExactParams& ep, bool tru
 // True when the small-M kernel has an instantiation for (MT, NT, C, NWK).
 bool exact_small_supported(int mt, int nt, int chunk, int nwk);
 // Digitize + small-M GEMM in one launch (exact_gemm_fused.hip): bf16 x [m, k] with row stride
-// ldx, packed weights, F <= 14, a small-M plan with MT = 1 and one split. hipErrorInvalidValue
-// for a plan it has no instantiation for.
-hipError_t launch_exact_fused(const ExactPlan& pl, const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw,
-                              void* out, int out_dtype, int64_t ldo, int64_t m, int64_t n, int64_t k, int f,
-                              bool trunc, hipStream_t st);
+// ldx, packed weights (cw used for F = 15), a small-M plan with MT = 1 and one split.
+// hipErrorInvalidValue for a plan it has no instantiation for, and for F = 15 where the
+// x-in-registers kernel does not apply.
+hipError_t launch_exact_fused(const ExactPlan& pl, const void* x, int64_t ldx, const int8_t* wp, const int32_t* cw,
+                              const int32_t* sw, void* out, int out_dtype, int64_t ldo, int64_t m, int64_t n,
+                              int64_t k, int f, bool trunc, hipStream_t st);
 // Packed operands only (exact_gemm_xw.hip).
 hipError_t launch_exact_xw(const ExactPlan& pl, const ExactParams& ep, bool trunc, hipStream_t st);
 bool exact_xw_supported(int bm, int bn, int r, int waves, bool trunc);

@@ -21,6 +21,7 @@ struct FusedParams {
   const uint16_t* x;  // bf16 [M, K], row stride ldx elements
   int64_t ldx;
   const int8_t* wp;  // packed weight digits
+  const int32_t* cw;  // weight digit sums (F = 15)
   const int32_t* sw;
   void* out;
   int64_t ldo;
@@ -313,13 +314,14 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
 // round trip before the first MFMA. The first round's weights are issued right after x and
 // arrive during the absmax; each later round's weights are issued before the MFMAs of the
 // round before it. Needs cdiv(KT, NWK) <= XS (the launcher picks XS).
-template <int NT, int NWK, int C, bool TRUNC, int XS>
+template <int NT, int NWK, int C, bool TRUNC, int XS, bool OFFSET>
 __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams p) {
   static_assert(XS % C == 0, "rounds of C steps");
   constexpr int BN = 16 * NT;
   constexpr int NR = XS / C;  // rounds
   __shared__ unsigned long long red[16 * BN];
   __shared__ float s_max[NWK][16];
+  __shared__ uint32_t s_cs[NWK][16];
   __shared__ float s_scale[16];
   __shared__ int32_t s_sh[16];
 
@@ -334,6 +336,7 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
   const int64_t n0 = bn * BN;
   const int mrows = (int)min<int64_t>(16, p.M - m0);
   const int64_t nsteps = p.KT;
+  // OFFSET (F = 15): offset digits, with the row digit sum cx (kernels.py:31-34)
 
   for (int i = threadIdx.x; i < 16 * BN; i += nthr) red[i] = 0ull;
 
@@ -421,6 +424,7 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
     mx[nt] = v4i{0, 0, 0, 0};
     ll[nt] = v4i{0, 0, 0, 0};
   }
+  uint32_t cs = 0;  // this lane's part of its row's digit sum (F = 15; wraps like the digitize kernels)
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     if (wave + (int64_t)NWK * r * C >= nsteps) break;  // this wave has no steps left
@@ -428,6 +432,7 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int i = r * C + c;
+      const int64_t c0 = (wave + (int64_t)NWK * i) * 64 + kq * 16;  // this lane's first column
       if (wave + (int64_t)NWK * i < nsteps) {
         uint32_t hw[4], lw[4];
 #pragma unroll
@@ -438,7 +443,18 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
             const uint32_t w = xw[i][(4 * q + b) >> 1];
             const float v = __uint_as_float(((4 * q + b) & 1) ? (w & 0xFFFF0000u) : (w << 16));
             int32_t hd, ld;
-            digits_balanced(v, scale, hd, ld);
+            if constexpr (OFFSET) {
+              // columns past K keep zero digits: the weights' padding digits are zero too, and
+              // the digitize kernels leave those columns out of the sum
+              hd = 0;
+              ld = 0;
+              if (c0 + 4 * q + b < p.K) {
+                digits_offset(v, scale, hd, ld);
+                cs += (uint32_t)(256 * hd + ld);
+              }
+            } else {
+              digits_balanced(v, scale, hd, ld);
+            }
             h4 |= ((uint32_t)hd & 255u) << (8 * b);
             l4 |= ((uint32_t)ld & 255u) << (8 * b);
           }
@@ -465,7 +481,13 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
     }
   }
 
-  // 5. Wave partials meet in LDS (exact int64 adds), then the epilogue.
+  // 5. Wave partials meet in LDS (exact int64 adds), then the epilogue; with offset digits the
+  // row sums meet too (the row's 4 lanes, then the waves, all mod 2^32).
+  if constexpr (OFFSET) {
+    cs += __shfl_xor(cs, 16);
+    cs += __shfl_xor(cs, 32);
+    if (kq == 0) s_cs[wave][r16] = cs;
+  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -481,17 +503,28 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
   for (int i = threadIdx.x; i < mrows * BN; i += nthr) {
     const int mr = i / BN;
     const int64_t n = n0 + i % BN;
-    if (n < p.N)
-      store_f32_as(p.out, p.out_dtype, (m0 + mr) * p.ldo + n, exact_epilogue((int64_t)red[i], s_sh[mr], p.sw[n]));
+    if (n < p.N) {
+      int64_t tot = (int64_t)red[i];
+      if constexpr (OFFSET) {  // 128 (cx + cw) + 128^2 K (kernels.py:96-97, 148-151)
+        uint32_t cx = 0;
+#pragma unroll
+        for (int w = 0; w < NWK; ++w) cx += s_cs[w][mr];
+        tot += 128 * ((int64_t)(int32_t)cx + (int64_t)p.cw[n]) + 128 * 128 * p.K;
+      }
+      store_f32_as(p.out, p.out_dtype, (m0 + mr) * p.ldo + n, exact_epilogue(tot, s_sh[mr], p.sw[n]));
+    }
   }
 }
 
 // Instantiations of the x-in-registers kernel that compile without scratch (gfx950 -O3):
 // 4 steps a wave with at most 8 waves (at most 212 VGPRs of their 256), or with 16 waves and
 // one column tile, or two with 3 dots (at most 127 of their 128); 8 steps with at most 8
-// waves and NT * C <= 2 (at most 245). Other shapes and longer K take the row-pass kernel.
-template <int NT, int NWK, int C, int XS, bool TRUNC>
+// waves and NT * C <= 2 (at most 245). F = 15 (offset digits, 4 dots) drops the shapes whose
+// digit sum would spill. Other shapes and longer K take the row-pass kernel.
+template <int NT, int NWK, int C, int XS, bool TRUNC, bool OFFSET>
 constexpr bool xreg_fits() {
+  // F = 15 runs 4 dots, and its digit sum needs a few more registers
+  if (OFFSET && (TRUNC || (NWK == 16 && C > 1) || NT * C > 4)) return false;
   if (XS == 4) return NWK <= 8 || NT == 1 || (NT == 2 && C == 1 && TRUNC);
   return XS == 8 && NWK <= 8 && NT * C <= 2;
 }
@@ -518,9 +551,17 @@ hipError_t launch(const FusedParams& fp, hipStream_t st) {
   // more workgroups than CUs the row-pass kernel (about 75 VGPRs) runs several per CU, which
   // hides more latency than the saved x read gains (measured on gate_up and the lm_head).
   const int64_t per_wave = blocks <= device_cus() ? cdiv<int64_t>(fp.KT, NWK) : INT64_MAX;
-#define VXA_XREG(XS_)                                                                                             if constexpr (XS_ % C == 0 && xreg_fits<NT, NWK, C, XS_, TRUNC>()) {                                                  if (per_wave <= XS_) {                                                                                            hipLaunchKernelGGL((exact_fused_xreg_kernel<NT, NWK, C, TRUNC, XS_>), dim3((unsigned)blocks), dim3(64 * NWK),                          0, st, fp);                                                                                  return hipGetLastError();                                                                                     }                                                                                                             }
-  VXA_XREG(4) VXA_XREG(8)
+#define VXA_XREG(XS_, OFF_)                                                                                      \
+  if constexpr (XS_ % C == 0 && xreg_fits<NT, NWK, C, XS_, TRUNC, OFF_>()) {                                \
+    if (per_wave <= XS_ && (fp.F == 15) == OFF_) {                                                            \
+      hipLaunchKernelGGL((exact_fused_xreg_kernel<NT, NWK, C, TRUNC, XS_, OFF_>), dim3((unsigned)blocks),     \
+                         dim3(64 * NWK), 0, st, fp);                                                        \
+      return hipGetLastError();                                                                               \
+    }                                                                                                       \
+  }
+  VXA_XREG(4, false) VXA_XREG(8, false) VXA_XREG(4, true) VXA_XREG(8, true)
 #undef VXA_XREG
+  if (fp.F == 15) return hipErrorInvalidValue;  // offset digits: the register path only
   if (fp.M <= 4)
     hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, true>), dim3((unsigned)blocks), dim3(64 * NWK), 0, st,
                        fp);
@@ -547,14 +588,15 @@ hipError_t dispatch(const ExactPlan& pl, const FusedParams& fp, hipStream_t st) 
 
 }  // namespace
 
-hipError_t launch_exact_fused(const ExactPlan& pl, const void* x, int64_t ldx, const int8_t* wp, const int32_t* sw,
-                              void* out, int out_dtype, int64_t ldo, int64_t m, int64_t n, int64_t k, int f,
-                              bool trunc, hipStream_t st) {
+hipError_t launch_exact_fused(const ExactPlan& pl, const void* x, int64_t ldx, const int8_t* wp, const int32_t* cw,
+                              const int32_t* sw, void* out, int out_dtype, int64_t ldo, int64_t m, int64_t n,
+                              int64_t k, int f, bool trunc, hipStream_t st) {
   if (pl.family != kFamilySmall || pl.mt != 1 || pl.sk != 1) return hipErrorInvalidValue;
   FusedParams fp;
   fp.x = reinterpret_cast<const uint16_t*>(x);
   fp.ldx = ldx;
   fp.wp = wp;
+  fp.cw = cw;
   fp.sw = sw;
   fp.out = out;
   fp.ldo = ldo;

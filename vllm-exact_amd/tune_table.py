@@ -12,7 +12,7 @@ candidate first, then the FINALISTS fastest in full (about 4 ms of calls per rep
 replays, 10 for the big lm_heads; the median counts). By default the weights
 are packed at load time and x is digitized packed, as exactmm::linear runs them (--layout
 plain tunes the row-major kernels instead), and the GEMM on digitized x is timed alone.
-Up to 64 rows on packed weights with F < 15, every cfg the one-launch digitize + GEMM
+Up to 64 rows on packed weights, every cfg the one-launch digitize + GEMM
 kernel takes is also timed on that path; it is chosen, and M listed in the row's
 "one_launch", when it beats digitize + the best two-launch GEMM timed together. The result
 is {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK], "one_launch": [M, ...]}}; with
@@ -77,7 +77,7 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
     for M in ms:
         x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
         xd = K.digitize_packed(x, F) if packed else K.digitize(x, F)
-        try_one = packed and F < 15 and M <= ONE_LAUNCH_TUNE_ROWS
+        try_one = packed and M <= ONE_LAUNCH_TUNE_ROWS
 
         def gemm(i, cfg, xd=xd):
             if packed:
@@ -145,7 +145,7 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
         rec["finalists"] = [[round(t, 2), list(c)] for t, c in tried]
         rec["finalists_one_launch"] = [[round(t, 2), list(c)] for t, c in tried_one]
         report.append(rec)
-    if packed and F < 15:
+    if packed:
         row["one_launch"] = one_rows
     del wds, wbs
     torch.cuda.empty_cache()

@@ -66,7 +66,7 @@ _SIGNATURES = {
     ),
     "vxa_exact_linear_bf16x": (
         _int,
-        [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int, _vp],
+        [_vp, _i64, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int, _vp],
     ),
     "vxa_paged_decode_workspace": (_int, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
     "vxa_paged_decode": (

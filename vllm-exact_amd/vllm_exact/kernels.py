@@ -217,9 +217,10 @@ def bf16x_rows_aligned(x):
 def exact_linear_bf16x(x, wp, K, F, trunc=False, out=None, cfg=None):
     """Digitize x (bf16 [M, K]) and run exact_linear_packed in one launch: the bits of
     exact_linear_packed(digitize_packed(x, F), wp, K, F, trunc, cfg=cfg). Raises
-    NotImplementedError where the one-launch path does not apply (F = 15, a cfg outside the
-    one-row-tile small-M family or with split-K, x rows not 16-byte aligned); the two-launch
-    path covers those."""
+    NotImplementedError where the one-launch path does not apply (a cfg outside the
+    one-row-tile small-M family or with split-K, x rows not 16-byte aligned, or F = 15 where
+    its x-in-registers kernel does not: 3 dots, more workgroups than CUs, K beyond its
+    registers); the two-launch path covers those."""
     pw, cw, sw = wp
     _require_gpu(x, "exact_linear_bf16x")
     if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
@@ -242,7 +243,8 @@ def exact_linear_bf16x(x, wp, K, F, trunc=False, out=None, cfg=None):
     arr, n = _nx.cfg_array(cfg)
     with torch.cuda.device(dev):
         _nx.check(_nx.lib().vxa_exact_linear_bf16x(
-            x.data_ptr(), x.stride(0), pw.data_ptr(), sw.data_ptr(), out.data_ptr(), _nx.dtype_enum(out.dtype),
+            x.data_ptr(), x.stride(0), pw.data_ptr(), cw.data_ptr(), sw.data_ptr(), out.data_ptr(),
+            _nx.dtype_enum(out.dtype),
             out.stride(0), M, N, K, int(F), int(bool(trunc)), arr, n, _nx.stream_handle(dev)), "exact_linear_bf16x")
     return out
 

@@ -84,7 +84,7 @@ def _one_launch(M, N, Kd):
     return M <= K.ONE_LAUNCH_MAX_ROWS
 
 
-# cfgs the one-launch digitize + GEMM path refused (two-row tiles, split-K, other families)
+# cfgs (at F = 15: cfg and shape) the one-launch digitize + GEMM path refused
 _ONE_LAUNCH_CFG = {}
 
 
@@ -111,15 +111,17 @@ def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: tor
         xb = x2[i:i + RB]
         cfg = _cfg(xb.shape[0], N, Kd)
         if packed:
-            if (xb.dtype == torch.bfloat16 and F < 15 and _one_launch(xb.shape[0], N, Kd)
-                    and _ONE_LAUNCH_CFG.get(cfg, True)):
+            # a refusal is the cfg's own at F < 15; at F = 15 it also depends on the grid and K
+            key = cfg if F < 15 else (cfg, N, Kd, xb.shape[0])
+            if (xb.dtype == torch.bfloat16 and _one_launch(xb.shape[0], N, Kd)
+                    and _ONE_LAUNCH_CFG.get(key, True)):
                 # digitize inside the GEMM launch where the cfg allows it (same bits, one launch fewer)
                 try:
                     K.exact_linear_bf16x(xb, (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
                     continue
                 except NotImplementedError:
                     if K.bf16x_rows_aligned(xb):
-                        _ONE_LAUNCH_CFG[cfg] = False  # refused for the cfg, not for this x
+                        _ONE_LAUNCH_CFG[key] = False  # refused for the cfg (and shape), not for this x
             K.exact_linear_packed(K.digitize_packed(xb, F), (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
         else:
             K.exact_linear(K.digitize(xb, F), (wh, wl, cw, sw), F, TRUNC, out=out[i:i + RB], cfg=cfg)
