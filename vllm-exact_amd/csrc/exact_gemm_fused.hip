@@ -313,7 +313,8 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
 // the waves through LDS), and the K loop converts them, so x costs one read and no second
 // round trip before the first MFMA. The first round's weights are issued right after x and
 // arrive during the absmax; each later round's weights are issued before the MFMAs of the
-// round before it. Needs cdiv(KT, NWK) <= XS (the launcher picks XS).
+// round before it. Needs cdiv(KT, NWK) <= XS (the launcher picks XS). OFFSET (F = 15): offset
+// digits, with each row's digit sum cx added in the epilogue (kernels.py:31-34, 96-97).
 template <int NT, int NWK, int C, bool TRUNC, int XS, bool OFFSET>
 __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams p) {
   static_assert(XS % C == 0, "rounds of C steps");
@@ -336,7 +337,6 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
   const int64_t n0 = bn * BN;
   const int mrows = (int)min<int64_t>(16, p.M - m0);
   const int64_t nsteps = p.KT;
-  // OFFSET (F = 15): offset digits, with the row digit sum cx (kernels.py:31-34)
 
   for (int i = threadIdx.x; i < 16 * BN; i += nthr) red[i] = 0ull;
 
@@ -412,10 +412,11 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
     s_sh[threadIdx.x] = sh;
   }
   __syncthreads();
-  const float scale = s_scale[r16];  // rows past M hold zeros: any scale gives zero digits
+  const float scale = s_scale[r16];  // rows past M: their results are never stored
 
   // 4. K loop.
-  constexpr bool kSplitMd = NT == 1 || (NT == 2 && NWK < 16);  // NT = 2 with 16 waves: one cross accumulator (128 VGPRs)
+  // the cross products in two accumulators, except NT = 2 with 16 waves (128 VGPRs a lane)
+  constexpr bool kSplitMd = NT == 1 || (NT == 2 && NWK < 16);
   v4i hh[NT], md[NT], mx[NT], ll[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
