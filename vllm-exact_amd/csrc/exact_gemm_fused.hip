@@ -520,14 +520,15 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
 // Instantiations of the x-in-registers kernel that compile without scratch (gfx950 -O3):
 // 4 steps a wave with at most 8 waves (at most 212 VGPRs of their 256), or with 16 waves and
 // one column tile, or two with 3 dots (at most 127 of their 128); 8 steps with at most 8
-// waves and NT * C <= 2 (at most 245). F = 15 (offset digits, 4 dots) drops the shapes whose
-// digit sum would spill. Other shapes and longer K take the row-pass kernel.
+// waves and NT * C <= 2, or four tiles with 3 dots (at most 252). F = 15 (offset digits,
+// 4 dots) drops the shapes whose digit sum would spill. Other shapes and longer K take the
+// row-pass kernel.
 template <int NT, int NWK, int C, int XS, bool TRUNC, bool OFFSET>
 constexpr bool xreg_fits() {
   // F = 15 runs 4 dots, and its digit sum needs a few more registers
   if (OFFSET && (TRUNC || (NWK == 16 && C > 1) || NT * C > 4)) return false;
   if (XS == 4) return NWK <= 8 || NT == 1 || (NT == 2 && C == 1 && TRUNC);
-  return XS == 8 && NWK <= 8 && NT * C <= 2;
+  return XS == 8 && NWK <= 8 && (NT * C <= 2 || (NT == 4 && C == 1 && TRUNC && !OFFSET));
 }
 
 // Compute units of the current device (cached per device; 0 when the query fails).
