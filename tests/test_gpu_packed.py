@@ -209,11 +209,11 @@ def test_op_row_blocks_and_input_layouts():
     assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape))
 
 
-def _shipped_entries():
-    """Distinct (M, K, cfg, one_launch) of the shipped table: cfgs only change speed, so each
+def _shipped_entries(path):
+    """Distinct (M, K, cfg, one_launch) of a shipped table: cfgs only change speed, so each
     runs on a small ragged N instead of its shape's."""
     import json
-    raw = json.loads(vllm_exact.TABLES["mi355x"].read_text())
+    raw = json.loads(path.read_text())
     out = set()
     for nk, row in raw.items():
         kd = int(nk.split(",")[1])
@@ -224,28 +224,30 @@ def _shipped_entries():
     return sorted(out)
 
 
-def test_every_shipped_table_entry_is_exact():
-    """Every entry of the shipped gfx950 table, at its own row count and K, gives the oracle's
-    bits; the entries marked one-launch also through the one-launch kernel."""
+@pytest.mark.parametrize("which,F,tr", [("F14", 14, True), ("F15", 15, False)])
+def test_every_shipped_table_entry_is_exact(which, F, tr):
+    """Every entry of a shipped gfx950 table (the one tuned at F = 14, and the one tuned at
+    F = 15 with 4 dots), at its own row count and K, gives the oracle's bits; the entries
+    marked one-launch also through the one-launch kernel."""
     N = 200  # ragged against every BN in the table
-    entries = _shipped_entries()
+    entries = _shipped_entries((vllm_exact.TABLES if which == "F14" else vllm_exact.TABLES_F15)["mi355x"])
     data = {}
     for M, Kd, cfg, one in entries:
         if (M, Kd) not in data:
             x, w = stress_xw(M, N, Kd, seed=M + Kd)
             x = x.to(torch.bfloat16)
-            xd_np = oracle.digitize_c(x.float().numpy(), plugin.F)
-            wd = K.digitize_packed(w.to(torch.bfloat16).to(DEV), plugin.F)
-            wd_np = oracle.digitize_c(w.to(torch.bfloat16).float().numpy(), plugin.F)
-            want = oracle.bf16_rne_c(oracle.exact_linear_c(xd_np, wd_np, plugin.F, plugin.TRUNC)).reshape(M, N)
+            xd_np = oracle.digitize_c(x.float().numpy(), F)
+            wd = K.digitize_packed(w.to(torch.bfloat16).to(DEV), F)
+            wd_np = oracle.digitize_c(w.to(torch.bfloat16).float().numpy(), F)
+            want = oracle.bf16_rne_c(oracle.exact_linear_c(xd_np, wd_np, F, tr)).reshape(M, N)
             data[(M, Kd)] = (x.to(DEV), wd, want)
         xg, wd, want = data[(M, Kd)]
         out = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
-        K.exact_linear_packed(K.digitize_packed(xg, plugin.F), wd, Kd, plugin.F, plugin.TRUNC, out=out, cfg=cfg)
+        K.exact_linear_packed(K.digitize_packed(xg, F), wd, Kd, F, tr, out=out, cfg=cfg)
         assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), want), (M, Kd, cfg)
         if one:
             out.zero_()
-            K.exact_linear_bf16x(xg, wd, Kd, plugin.F, plugin.TRUNC, out=out, cfg=cfg)
+            K.exact_linear_bf16x(xg, wd, Kd, F, tr, out=out, cfg=cfg)
             assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), want), (M, Kd, cfg, "one")
     assert len(entries) > 50
 

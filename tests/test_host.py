@@ -75,8 +75,8 @@ def test_tuner_merge_keeps_untuned_entries():
     assert tune.merge_row({}, {"64": c, "one_launch": []}, [64]) == {"64": c, "one_launch": []}
 
 
-def test_shipped_table_is_well_formed():
-    path = vllm_exact.TABLES["mi355x"]
+@pytest.mark.parametrize("path", [vllm_exact.TABLES["mi355x"], vllm_exact.TABLES_F15["mi355x"]])
+def test_shipped_table_is_well_formed(path):
     raw = json.loads(path.read_text())
     for nk, row in raw.items():
         n, k = map(int, nk.split(","))

@@ -22,6 +22,8 @@ __version__ = "0.1.0"
 _ENABLED = False
 # Tuning tables ship for MI355X only; the reference's H200/B300 tables describe other GPUs.
 TABLES = {"mi355x": Path(__file__).with_name("cfg_table_mi355x_F14.json")}
+# Tuned at F = 15 (offset digits, 4 dots): enable(f=15) takes it for the same key.
+TABLES_F15 = {"mi355x": Path(__file__).with_name("cfg_table_mi355x_F15.json")}
 
 
 def _attention_backends():
@@ -36,7 +38,7 @@ def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x"
     max_model_len: the value passed to LLM (fixes the attention kernel's segment count).
     f: 14 (truncated, 3 INT8 dots; default) or 15 (offset digits, 4 dots).
     cfg_table: "mi355x", a path to a table, or None (built-in configs). Tables change speed
-      only, never results.
+      only, never results. "mi355x" means the table tuned at F = 15 when f = 15.
     max_num_batched_tokens: must exceed every prompt length (prompts are never chunked).
     attention_backend: the vLLM backend whose decode path is replaced (paged_attn.BACKENDS;
       the reference always uses FLASH_ATTN). vLLM is asked for the same backend.
@@ -63,7 +65,8 @@ def enable(max_model_len, f=14, lm_head=True, attention=True, cfg_table="mi355x"
     plugin.TRUNC = f == 14
     plugin.LMHEAD = lm_head
     plugin.RELEASE_WEIGHTS = bool(release_weights)
-    plugin.load_table(TABLES.get(cfg_table, cfg_table) if cfg_table else None)
+    tables = TABLES_F15 if f == 15 else TABLES
+    plugin.load_table(tables.get(cfg_table, cfg_table) if cfg_table else None)
 
     from vllm.v1.attention.backends.gdn_attn import GDNAttentionBackend
     GDNAttentionBackend.supports_batch_invariance = classmethod(lambda cls: True)
