@@ -4,9 +4,9 @@
     python bench.py --profile-kernel [--steps K]   (launches for rocprofv3 counter runs)
     python bench.py --profile-counters             (every sweep GEMM and attention shape, for counter runs)
 
-Step: one pass of the decode-shaped exact linear sweep (the BASELINE workload for this
-metric): QKV 4096->6144, O 4096->4096, gate_up 4096->24576 and down 12288->4096 at
-M in {1, 16, 64, 256}, F = 14 truncated (3 INT8 dots, the enable() default), each through
+Step: one pass of the decode-shaped exact linear sweep of a ~9B Qwen-style model (hidden
+4096): QKV 4096->6144, O 4096->4096, gate_up 4096->24576 and down 12288->4096 at M in
+{1, 16, 64, 256}, F = 14 truncated (3 INT8 dots, the enable() default), each through
 the full exactmm::linear path (bf16 x -> digitize -> exact GEMM -> bf16 y). The step is a
 HIP graph; weights rotate over copies so no use finds its weights in the MALL/L2; inputs
 sit in HBM before timing starts. `value` is the sweep's algorithmic bytes
@@ -439,7 +439,7 @@ def main():
 
     # ---------------------------------------------------------------- bit-exactness of the outputs
     sys.path.insert(0, str(ROOT / "oracle"))
-    import oracle  # the checker only
+    import oracle  # CPU oracle: checks the outputs, never computes them
 
     exact_ok = True
     for M, name, N, Kd in [(16, "o", 4096, 4096), (256, "down", 4096, 12288), (1, "qkv", 6144, 4096)]:
@@ -481,7 +481,7 @@ def main():
             del kv, kc, vc
             torch.cuda.empty_cache()
 
-    # ---------------------------------------------------------------- exact lm_head (config 3)
+    # ---------------------------------------------------------------- exact lm_head 4096 -> 151936
     lm_head = []
     if not args.no_lm_head:
         N, Kd = VOCAB, HIDDEN

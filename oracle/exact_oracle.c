@@ -2,7 +2,7 @@
  * exact_oracle.c -- CPU oracle for the exact linear path. TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library,
- * and only as the checker (or as the timed CPU baseline). The product path never calls it.
+ * and only to check results (or as the timed CPU baseline). The product path never calls it.
  *
  * It restates, in plain C, the reference's CPU arithmetic:
  *   oracle_digitize_f32      <- kernels.py:22-39 (digitize_torch); exponent via frexp as

@@ -1,7 +1,7 @@
 """CPU oracle for the exact linear path. TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module,
-and only as the checker (or as the timed CPU baseline); the product never does.
+and only to check results (or as the timed CPU baseline); the product never does.
 
 Two independent restatements of the reference's CPU arithmetic:
 * numpy (this file): digitize_np <- kernels.py:22-39, exact_linear_np <- kernels.py:89-100,

@@ -2,8 +2,8 @@
 
 Restates the reference's tests/test_gpu.py:46-78 (error against a float reference,
 computing only the first n requests leaves them bitwise unchanged, moving physical pages
-with the block table remapped leaves the output bitwise unchanged) and adds the BASELINE
-shapes (H=32, KV=8, D=128, block size 16 at batch 64 x 8K, 16 x 16K and 256 x 1K), where each
+with the block table remapped leaves the output bitwise unchanged) and adds the decode
+shapes of a ~9B model's full-attention layer (H=32, KV=8, D=128, block size 16 at batch 64 x 8K, 16 x 16K and 256 x 1K), where each
 request run alone must give the bits it gets inside mixed batches.
 
 Stated tolerance against the float64 oracle (V ~ N(0, 1) or 0.5 N(0, 1)):

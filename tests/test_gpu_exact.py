@@ -2,7 +2,7 @@
 
 Restates the reference's tests/test_gpu.py:13-43 (every tiling and split-K partition equals
 the CPU integer reference; bf16 output equals the fp32 output cast to bf16; bf16 input
-digitizes like its fp32 upcast) and extends them to the BASELINE shapes:
+digitizes like its fp32 upcast) and extends them to the decode shapes of a ~9B model:
 * M=16, K=N=4096, 4 dots, no split-K (CPU-runnable configuration): full output;
 * decode-shaped QKV/O/gate_up/down at M in {1, 16, 64, 256}, 3 and 4 dots, every split-K
   factor in {1, 2, 4, 8} and every tile config: all bits equal each other and the oracle

@@ -209,6 +209,22 @@ def test_op_row_blocks_and_input_layouts():
     assert np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape))
 
 
+@pytest.mark.parametrize("M", [3, 64, 257])
+def test_op_fp16_activations(M):
+    """fp16 activations, the reference's other supported dtype (plugin.py:113-114): the op
+    digitizes the fp16 values and writes fp16 output (x.dtype), the fp32 result rounded once
+    to nearest even. 3 rows would take the one-launch path for bf16; fp16 goes in two."""
+    g = torch.Generator().manual_seed(12)
+    w = (torch.randn(200, 1024, generator=g) * 0.02).to(torch.bfloat16)
+    wbuf = plugin.pack_weight(w.to(DEV))
+    x = (torch.randn(M, 1024, generator=g) * 4).to(torch.float16)
+    y = torch.ops.exactmm.linear(x.to(DEV), *wbuf)
+    assert y.dtype == torch.float16 and y.shape == (M, 200)
+    ref = oracle.exact_linear_c(oracle.digitize_c(x.float().numpy(), plugin.F),
+                                oracle.digitize_c(w.float().numpy(), plugin.F), plugin.F, plugin.TRUNC)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
 def _shipped_entries(path):
     """Distinct (M, K, cfg, one_launch) of a shipped table: cfgs only change speed, so each
     runs on a small ragged N instead of its shape's."""
