@@ -78,9 +78,11 @@ def test_device_count_limits_the_requests(L):
         P.paged_decode(q, kc, vc, bt, sl, scale, out, B, 0, n_live=torch.tensor([1], device=DEV))
 
 
-@pytest.mark.parametrize("B,L,BS", [(8, 300, 16), (8, 5000, 528), (4, 9000, 528), (64, 8192, 528)])
+@pytest.mark.parametrize("B,L,BS", [(8, 300, 16), (8, 5000, 528), (4, 9000, 528), (64, 8192, 528), (8, 3000, 8),
+                                    (6, 2000, 24)])
 def test_paged_attention_reference_cases(B, L, BS):
-    """tests/test_gpu.py:57-78: H=16, KV=4, D=256, cache x0.5, scale 1/16."""
+    """tests/test_gpu.py:57-78: H=16, KV=4, D=256, cache x0.5, scale 1/16. Page sizes 8 and 24
+    (below 16, and not a power of two) take the per-key page lookup."""
     H, KV, D = 16, 4, 256
     q, kv, bt, sl = make_paged(B, L, BS, H, KV, D, seed=0, kv_scale=0.5)
     q, kv, bt, sl = q.to(DEV), kv.to(DEV), bt.to(DEV), sl.to(DEV)
