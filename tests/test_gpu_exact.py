@@ -81,9 +81,11 @@ def test_digitize_strided_rows():
 
 # ------------------------------------------------------------------ exact GEMM
 @pytest.mark.parametrize("F,tr", [(14, True), (15, False), (14, False), (15, True)])
-@pytest.mark.parametrize("M,N,Kd", [(24, 384, 4096), (5, 200, 12288), (1, 64, 4096), (300, 256, 12288)])
+@pytest.mark.parametrize("M,N,Kd", [(24, 384, 4096), (5, 200, 12288), (1, 64, 4096), (300, 256, 12288),
+                                    (7, 201, 4096)])
 def test_exact_linear_split_k_bitwise(F, tr, M, N, Kd):
-    """tests/test_gpu.py:13-32: every cfg x SK x mma equals the CPU integer reference."""
+    """tests/test_gpu.py:13-32: every cfg x SK x mma equals the CPU integer reference. An odd N
+    takes the split-K finalize's one-column loads."""
     x, w = stress_xw(M, N, Kd)
     xd, wd = K.digitize(x.to(DEV), F), K.digitize(w.to(DEV), F)
     ref = oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr)

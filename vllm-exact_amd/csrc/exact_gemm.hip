@@ -8,15 +8,36 @@ namespace {
 
 // Split-K finalize: sum the int64 partials of every split in a fixed order (any order gives
 // the same integer), add the offset terms once, apply the epilogue (kernels.py:159-177).
-__global__ __launch_bounds__(256) void exact_finalize_kernel(ExactParams p) {
+// Grid: x over column pairs (two outputs a lane, one 16-byte load a split when N is even),
+// y over rows (grid-stride past 65535 rows).
+constexpr int kFinThreads = 256;
+__global__ __launch_bounds__(kFinThreads) void exact_finalize_kernel(ExactParams p) {
   const int64_t mn = p.M * p.N;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < mn;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t m = idx / p.N, n = idx % p.N;
-    int64_t tot = 0;
-    for (int s = 0; s < p.sk; ++s) tot += p.ws[s * mn + idx];
-    if (p.offset) tot += offset_terms(p, m, n);
-    store_f32_as(p.out, p.out_dtype, m * p.ldo + n, exact_epilogue(tot, p.sx[m], p.sw[n]));
+  const int64_t n0 = ((int64_t)blockIdx.x * kFinThreads + threadIdx.x) * 2;
+  if (n0 >= p.N) return;
+  const bool two = n0 + 1 < p.N;
+  const bool vec = (p.N & 1) == 0 && ((uintptr_t)p.ws & 15) == 0;  // every pair 16-byte aligned
+  for (int64_t m = blockIdx.y; m < p.M; m += gridDim.y) {
+    const int64_t idx = m * p.N + n0;
+    int64_t t0 = 0, t1 = 0;
+    if (vec) {
+      for (int s = 0; s < p.sk; ++s) {
+        const longlong2 v = *reinterpret_cast<const longlong2*>(p.ws + s * mn + idx);
+        t0 += v.x;
+        t1 += v.y;
+      }
+    } else {
+      for (int s = 0; s < p.sk; ++s) {
+        t0 += p.ws[s * mn + idx];
+        if (two) t1 += p.ws[s * mn + idx + 1];
+      }
+    }
+    if (p.offset) t0 += offset_terms(p, m, n0);
+    store_f32_as(p.out, p.out_dtype, m * p.ldo + n0, exact_epilogue(t0, p.sx[m], p.sw[n0]));
+    if (two) {
+      if (p.offset) t1 += offset_terms(p, m, n0 + 1);
+      store_f32_as(p.out, p.out_dtype, m * p.ldo + n0 + 1, exact_epilogue(t1, p.sx[m], p.sw[n0 + 1]));
+    }
   }
 }
 
@@ -130,6 +151,9 @@ namespace {
 // Launch the GEMM kernels (and the split-K finalize) for a filled-in ExactParams.
 int run_exact(const ExactPlan& pl, ExactParams& ep, int trunc, bool packed, bool vec_ok, hipStream_t st) {
   hipError_t err;
+  const int64_t fin_bx = cdiv<int64_t>(ep.N, 2 * kFinThreads);  // finalize grid: column pairs x rows
+  const int64_t fin_by = ep.M < 65535 ? ep.M : 65535;
+  if (pl.sk > 1 && fin_bx > 0x7FFFFFFFLL) return VXA_ERR_UNSUPPORTED;
   if (!vec_ok) {
     if (ep.M > 65535 || pl.sk > 65535) return VXA_ERR_UNSUPPORTED;
     dim3 grid((unsigned)cdiv<int64_t>(ep.N, 256), (unsigned)ep.M, (unsigned)pl.sk);
@@ -151,9 +175,8 @@ int run_exact(const ExactPlan& pl, ExactParams& ep, int trunc, bool packed, bool
   if (err == hipErrorInvalidValue) return VXA_ERR_UNSUPPORTED;
   if (err != hipSuccess) return VXA_ERR_LAUNCH;
   if (pl.sk > 1) {
-    const int64_t fb = cdiv<int64_t>(ep.M * ep.N, 256);
-    const int64_t blocks = fb < 65536 ? fb : 65536;
-    hipLaunchKernelGGL(exact_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, st, ep);
+    hipLaunchKernelGGL(exact_finalize_kernel, dim3((unsigned)fin_bx, (unsigned)fin_by), dim3(kFinThreads), 0, st,
+                       ep);
     if (hipGetLastError() != hipSuccess) return VXA_ERR_LAUNCH;
   }
   return VXA_OK;
