@@ -123,6 +123,17 @@ def test_exact_linear_ragged_k_scalar_path():
             assert np.array_equal(f32_bits(K.exact_linear(xd, wd, F, tr, cfg=cfg).cpu().numpy()), ref)
 
 
+def test_exact_linear_rows_past_grid_y_limit_split_k():
+    """66000 rows with split-K 2: the finalize grid covers at most 65535 rows per y and strides
+    over the rest; every row equals the oracle."""
+    x, w = stress_xw(66000, 18, 256, seed=5)
+    F, tr = 14, True
+    xd, wd = K.digitize(x.to(DEV), F), K.digitize(w.to(DEV), F)
+    ref = f32_bits(oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr))
+    for cfg in ((16, 16, 128, 4, 1, 8, 2), (64, 64, 128, 4, 4, 8, 2)):
+        assert np.array_equal(f32_bits(K.exact_linear(xd, wd, F, tr, cfg=cfg).cpu().numpy()), ref), cfg
+
+
 def test_config1_single_linear_bitwise():
     """M=16, K=N=4096, bf16 x ~ N(0,1), w ~ N(0,0.02), seed 0, F=14 4 dots, no split-K."""
     x, w = xw(16, 4096, 4096, seed=0, outlier=False)
