@@ -135,7 +135,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode-step", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
                     help="exact_int8 tuning table to use")
     ap.add_argument("--profile-counters", action="store_true",
@@ -587,7 +587,7 @@ def main():
                 oracle.exact_linear_c(xdn, wd, F, TRUNC)
                 reps += 1
                 dt = (time.perf_counter() - t0) / reps
-                if reps * dt >= min_s / 4 or reps >= 50:
+                if reps * dt >= min_s or reps >= 5000:
                     break
             total_s += dt * N / ns
             cpu_op_s[(M, name)] = dt * N / ns
