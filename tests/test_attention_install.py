@@ -69,6 +69,8 @@ def backend(monkeypatch):
         ENCODER_ONLY = "encoder_only"
 
     class FlashAttentionBackend:
+        forward_includes_kv_cache_update = False  # new keys/values are stored outside forward
+
         @staticmethod
         def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size, cache_dtype_str="auto"):
             if block_size % 16:
@@ -154,3 +156,26 @@ def test_enable_checks_the_backend_name(monkeypatch):
     with pytest.raises(ValueError, match="attention_backend"):
         vllm_exact.enable(1024, attention_backend="NO_SUCH_BACKEND")
     assert not vllm_exact._ENABLED
+
+
+def test_install_refuses_backends_that_write_the_cache_in_forward(backend):
+    """Decode-only steps skip the backend's forward, so a backend whose forward stores the new
+    token's key and value (or that does not say where it stores them) is refused."""
+    mod, _ = backend
+    original = mod.FlashAttentionImpl.forward
+    mod.FlashAttentionBackend.forward_includes_kv_cache_update = True
+    with pytest.raises(NotImplementedError, match="outside forward"):
+        P.install("FLASH_ATTN")
+    del mod.FlashAttentionBackend.forward_includes_kv_cache_update  # older vLLM: no flag at all
+    with pytest.raises(NotImplementedError, match="outside forward"):
+        P.install("FLASH_ATTN")
+    mod.FlashAttentionImpl.do_kv_cache_update = lambda self, *a: None  # ... but a separate cache step
+    assert P.install("FLASH_ATTN") is original
+    mod.FlashAttentionImpl.forward = original
+
+
+def test_install_offers_no_backend_with_an_undeclared_physical_layout():
+    """vLLM's ROCM_ATTN reads K through an x-packed layout its declared shape does not show."""
+    assert "ROCM_ATTN" not in P.BACKENDS
+    with pytest.raises(ValueError, match="backend must be one of"):
+        P.install("ROCM_ATTN")

@@ -139,7 +139,7 @@ def test_fused_path_declines_and_the_op_falls_back():
                               oracle.bf16_rne_c(ref).reshape(ref.shape)), M
 
 
-@pytest.mark.parametrize("shape", [(6144, 4096), (24576, 4096), (4096, 12288)])
+@pytest.mark.parametrize("shape", [(6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)])
 def test_op_with_packed_weights_matches_oracle(shape):
     N, Kd = shape
     g = torch.Generator().manual_seed(3)

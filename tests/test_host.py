@@ -181,3 +181,31 @@ def test_paged_decode_torch_matches_oracle():
     bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
     want = oracle.paged_decode_c(bits(q), bits(kc), bits(vc), bt.numpy(), sl.numpy(), 0.125, 3)
     np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_plugin_classes_register_and_dispatch(monkeypatch):
+    """The vLLM side of the plugin (plugin.py:87-133 of the reference), run on stand-in vLLM
+    base classes: the config registers as "exact_int8", reports bf16/fp16 activations and
+    capability 80, and hands ExactLinearMethod to every linear layer and ExactLMHeadMethod to
+    the lm_head only when LMHEAD is set; other layers get None."""
+    import vllm_standin as V
+
+    registry = V.install(monkeypatch)
+    lin_m, head_m, cfg_cls = plugin.define_vllm_classes()
+    assert registry == {"exact_int8": cfg_cls}
+    assert issubclass(lin_m, V.UnquantizedLinearMethod) and issubclass(head_m, V.UnquantizedEmbeddingMethod)
+    cfg = cfg_cls.from_config({})
+    assert isinstance(cfg, V.QuantizationConfig) and cfg.get_name() == "exact_int8"
+    assert cfg.get_supported_act_dtypes() == [torch.bfloat16, torch.float16]
+    assert cfg_cls.get_min_capability() == 80 and cfg_cls.get_config_filenames() == []
+
+    class QKV(V.LinearBase):
+        pass
+
+    monkeypatch.setattr(plugin, "LMHEAD", True)
+    assert type(cfg.get_quant_method(QKV(), "model.layers.0.qkv")) is lin_m
+    assert type(cfg.get_quant_method(V.ParallelLMHead(), "lm_head")) is head_m
+    assert cfg.get_quant_method(V.VocabParallelEmbedding(), "embed_tokens") is None
+    monkeypatch.setattr(plugin, "LMHEAD", False)
+    assert cfg.get_quant_method(V.ParallelLMHead(), "lm_head") is None
+    assert type(cfg.get_quant_method(QKV(), "model.layers.0.qkv")) is lin_m

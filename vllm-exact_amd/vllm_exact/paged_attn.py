@@ -88,33 +88,51 @@ def paged_decode(query, key_cache, value_cache, block_table, seq_lens, scale, ou
 
 
 def paged_decode_torch(query, key_cache, value_cache, block_table, seq_lens, scale, n):
-    """fp32 torch statement of the same attention (paged_attn.py:117-132): per request,
-    gather its keys/values through the block table, softmax(K q * scale) V per head."""
-    BS = key_cache.shape[1]
+    """fp32 torch statement of the same attention (paged_attn.py:117-132): for each request,
+    the keys and values of its seq_lens[b] tokens are collected once through its block-table
+    row, and each KV head's G query heads attend to them together as one batched product,
+    softmax(q_g K_g^T * scale) V_g. Returns fp32 (n, H, D)."""
+    page = key_cache.shape[1]
     H, D = query.shape[1], query.shape[2]
     KV = key_cache.shape[2]
     G = H // KV
     out = torch.empty(n, H, D, device=query.device, dtype=torch.float32)
     for b in range(n):
         L = int(seq_lens[b])
-        pos = torch.arange(L, device=query.device)
-        pages = block_table[b, pos // BS].long()
-        k = key_cache[pages, pos % BS].float()  # (L, KV, D)
-        v = value_cache[pages, pos % BS].float()
-        for h in range(H):
-            logits = (k[:, h // G] @ query[b, h].float()) * scale
-            out[b, h] = torch.softmax(logits, 0) @ v[:, h // G]
+        tok = torch.arange(L, device=query.device)
+        blk = block_table[b].long()[tok // page]
+        slot = tok % page
+        # (KV, L, D) per cache: token rows of each KV head
+        keys = key_cache[blk, slot].float().permute(1, 0, 2).contiguous()
+        vals = value_cache[blk, slot].float().permute(1, 0, 2).contiguous()
+        q = query[b].float().view(KV, G, D)
+        scores = torch.bmm(q, keys.transpose(1, 2).contiguous()) * scale  # (KV, G, L)
+        out[b] = torch.bmm(torch.softmax(scores, dim=-1), vals).reshape(H, D)
     return out
 
 
 # vLLM attention backends install() can wrap: name -> (module, impl class, backend class).
 # The reference patches FLASH_ATTN only (paged_attn.py:135-163); on ROCm vLLM may route
-# decode through TRITON_ATTN or ROCM_ATTN, whose KV caches are laid out differently.
+# decode through TRITON_ATTN, whose KV cache stacks K and V on an axis of its own. vLLM's
+# ROCM_ATTN backend is not offered: it declares a (2, blocks, page, heads, dim) shape but
+# reads and writes K through an x-packed layout ([blocks, heads, dim / x, page, x]), so views
+# taken from its declared shape would read K at the wrong offsets.
 BACKENDS = {
     "FLASH_ATTN": ("vllm.v1.attention.backends.flash_attn", "FlashAttentionImpl", "FlashAttentionBackend"),
     "TRITON_ATTN": ("vllm.v1.attention.backends.triton_attn", "TritonAttentionImpl", "TritonAttentionBackend"),
-    "ROCM_ATTN": ("vllm.v1.attention.backends.rocm_attn", "RocmAttentionImpl", "RocmAttentionBackend"),
 }
+
+
+def writes_cache_outside_forward(backend_cls, impl_cls):
+    """True when the backend stores new keys and values in the KV cache outside its forward:
+    it declares forward_includes_kv_cache_update = False, or, where vLLM has no such flag,
+    its impl has the separate do_kv_cache_update step. install() skips the backend's forward
+    on decode-only steps (as the reference does), so a backend that writes the cache inside
+    forward would never store the new token's key and value."""
+    flag = getattr(backend_cls, "forward_includes_kv_cache_update", None)
+    if flag is not None:
+        return not flag
+    return callable(getattr(impl_cls, "do_kv_cache_update", None))
 
 
 def kv_cache_views(shape_of, num_kv_heads, head_size):
@@ -174,13 +192,20 @@ def install(backend="FLASH_ATTN"):
     A request's attention output is then always computed by the same kernel in the same
     order, whatever the rest of the batch is. The wrapped backend must write new keys and
     values to the cache outside forward, as the reference's vLLM does: on decode-only steps
-    the backend's forward is not called."""
+    the backend's forward is not called. A backend that does not say so
+    (writes_cache_outside_forward) is refused with NotImplementedError."""
     import importlib
 
+    if backend not in BACKENDS:
+        raise ValueError(f"install: backend must be one of {sorted(BACKENDS)}, got {backend!r}")
     module_name, impl_name, backend_name = BACKENDS[backend]
     module = importlib.import_module(module_name)
     impl_cls = getattr(module, impl_name)
     backend_cls = getattr(module, backend_name)
+    if not writes_cache_outside_forward(backend_cls, impl_cls):
+        raise NotImplementedError(
+            f"install: {backend_name} does not declare that it writes the KV cache outside forward; decode-only "
+            "steps skip its forward, so the new token's key and value would never be stored")
     decoder = module.AttentionType.DECODER
     original = impl_cls.forward
     splits = {}

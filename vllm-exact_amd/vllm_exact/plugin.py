@@ -12,15 +12,6 @@ import torch
 
 from . import kernels as K
 
-try:  # vLLM is the host engine; it is not needed for the op itself
-    from vllm.model_executor.layers.linear import LinearBase, UnquantizedLinearMethod
-    from vllm.model_executor.layers.quantization import register_quantization_config
-    from vllm.model_executor.layers.quantization.base_config import QuantizationConfig
-    from vllm.model_executor.layers.vocab_parallel_embedding import ParallelLMHead, UnquantizedEmbeddingMethod
-    HAVE_VLLM = True
-except ImportError:
-    HAVE_VLLM = False
-
 # set by enable()
 F = 14
 TRUNC = True
@@ -40,6 +31,7 @@ def load_table(path):
     tuned row counts at which the op digitizes inside the GEMM launch (see _one_launch)."""
     global _TABLE
     _ONE_LAUNCH_ROWS.clear()
+    _ONE_LAUNCH_CFG.clear()
     if path is None:
         _TABLE = None
         return
@@ -84,8 +76,14 @@ def _one_launch(M, N, Kd):
     return M <= K.ONE_LAUNCH_MAX_ROWS
 
 
-# cfgs (at F = 15: cfg and shape) the one-launch digitize + GEMM path refused
+# (F, trunc, cfg, N, K[, M at F = 15]) the one-launch digitize + GEMM path refused. At F < 15
+# a refusal depends on the cfg and K (a K past 32768 columns needs a second K split); at F = 15
+# also on the grid, hence the row count. Cleared by load_table.
 _ONE_LAUNCH_CFG = {}
+
+
+def _one_launch_key(cfg, M, N, Kd):
+    return (F, TRUNC, tuple(cfg), N, Kd) + ((M,) if F == 15 else ())
 
 
 @torch.library.custom_op("exactmm::linear", mutates_args=())
@@ -111,8 +109,7 @@ def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: tor
         xb = x2[i:i + RB]
         cfg = _cfg(xb.shape[0], N, Kd)
         if packed:
-            # a refusal is the cfg's own at F < 15; at F = 15 it also depends on the grid and K
-            key = cfg if F < 15 else (cfg, N, Kd, xb.shape[0])
+            key = _one_launch_key(cfg, xb.shape[0], N, Kd)
             if (xb.dtype == torch.bfloat16 and _one_launch(xb.shape[0], N, Kd)
                     and _ONE_LAUNCH_CFG.get(key, True)):
                 # digitize inside the GEMM launch where the cfg allows it (same bits, one launch fewer)
@@ -174,9 +171,19 @@ def _apply(layer, x, bias):
     return y if bias is None else y + bias
 
 
-if HAVE_VLLM:
+def define_vllm_classes():
+    """Define ExactLinearMethod, ExactLMHeadMethod and ExactInt8Config on vLLM's own base
+    classes and register the config as quantization="exact_int8" (plugin.py:87-133). Runs at
+    import when vLLM is importable (ImportError otherwise); returns the three classes."""
+    from vllm.model_executor.layers.linear import LinearBase, UnquantizedLinearMethod
+    from vllm.model_executor.layers.quantization import register_quantization_config
+    from vllm.model_executor.layers.quantization.base_config import QuantizationConfig
+    from vllm.model_executor.layers.vocab_parallel_embedding import ParallelLMHead, UnquantizedEmbeddingMethod
 
     class ExactLinearMethod(UnquantizedLinearMethod):
+        """Every linear layer: weights digitized and packed once loaded, the product through
+        the exactmm::linear op (plugin.py:87-93)."""
+
         def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
             _digitize_layer(layer, release=RELEASE_WEIGHTS)
 
@@ -185,7 +192,7 @@ if HAVE_VLLM:
 
     class ExactLMHeadMethod(UnquantizedEmbeddingMethod):
         """lm_head through the exact linear layer; the embedding lookup is unchanged. Its bf16
-        weight is always kept: a tied lm_head shares it with the embedding."""
+        weight is always kept: a tied lm_head shares it with the embedding (plugin.py:96-102)."""
 
         def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
             _digitize_layer(layer)
@@ -222,3 +229,12 @@ if HAVE_VLLM:
             if LMHEAD and isinstance(layer, ParallelLMHead):
                 return ExactLMHeadMethod()
             return None
+
+    return ExactLinearMethod, ExactLMHeadMethod, ExactInt8Config
+
+
+try:  # vLLM is the host engine; the op and the helpers above do not need it
+    ExactLinearMethod, ExactLMHeadMethod, ExactInt8Config = define_vllm_classes()
+    HAVE_VLLM = True
+except ImportError:
+    HAVE_VLLM = False
