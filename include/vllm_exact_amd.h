@@ -23,15 +23,16 @@
 extern "C" {
 #endif
 
-/* Status codes. The Python binding maps ERR_ARG to ValueError, ERR_UNSUPPORTED to
- * NotImplementedError (so autotune/tuners can skip a config, kernels.py:313-314), and the
- * rest to RuntimeError. */
+/* Status codes. The Python binding maps ERR_ARG and ERR_TOO_LARGE to ValueError,
+ * ERR_UNSUPPORTED to NotImplementedError (so autotune/tuners can skip a config,
+ * kernels.py:313-314), and the rest to RuntimeError. */
 enum {
   VXA_OK = 0,
   VXA_ERR_ARG = 1,          /* bad pointer / size / stride / F / dtype */
   VXA_ERR_UNSUPPORTED = 2,  /* shape or config outside what the kernels implement */
   VXA_ERR_WORKSPACE = 3,    /* workspace missing or smaller than the plan requires */
-  VXA_ERR_LAUNCH = 4        /* hipLaunchKernel / hipGetLastError failure */
+  VXA_ERR_LAUNCH = 4,       /* hipLaunchKernel / hipGetLastError failure */
+  VXA_ERR_TOO_LARGE = 5     /* needs more than the fixed scratch of vxa_exact_linear_op_noalloc */
 };
 
 /* Element types of floating-point tensors crossing the boundary. */
@@ -193,6 +194,31 @@ int vxa_paged_decode_prefix(const void* q, int64_t sqt, int64_t sqh,
                             int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                             int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws,
                             size_t ws_bytes, vxa_stream_t stream);
+
+/* Bytes of device memory vxa_exact_linear_op_noalloc holds per GPU (a file-scope array). */
+#define VXA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * The exactmm::linear op with no allocation: vxa_digitize_packed of x followed by
+ * vxa_exact_linear_packed, the same bits, with the packed activation digits, their row sums
+ * and shifts, and the split-K partials kept in a fixed array of VXA_NOALLOC_SCRATCH_BYTES that
+ * the library holds on each GPU until the process ends. Calls no hipMalloc or hipFree.
+ *   x      [m, k] activations, dtype VXA_F32 / VXA_BF16 / VXA_F16, row stride ldx elements
+ *   wp, cw, sw, out, cfg   as vxa_exact_linear_packed
+ * Needs vxa_packed_bytes(m, k) + 8 m (each part rounded up to 256 bytes) + the planned split-K
+ * workspace to fit the array; larger problems return VXA_ERR_TOO_LARGE before any launch (for
+ * example 4096 rows of 4096 columns, or a split-K plan over 256 x 151936 outputs).
+ * Every call on one GPU uses that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller. The first call on each device looks the
+ * array's device address up; make it outside graph capture.
+ * No counterpart in the reference (which allocates the digits and the split-K workspace with
+ * torch.empty, kernels.py:78-80, 273): for callers that cannot allocate, such as code under
+ * HIP graph capture, fixed serving loops and harnesses that forbid allocation.
+ */
+int vxa_exact_linear_op_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* wp,
+                                const int32_t* cw, const int32_t* sw, void* out, int out_dtype,
+                                int64_t ldo, int64_t m, int64_t n, int64_t k, int f, int trunc,
+                                const int32_t* cfg, int cfg_len, vxa_stream_t stream);
 
 #ifdef __cplusplus
 }

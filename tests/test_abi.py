@@ -149,3 +149,21 @@ def test_fused_entry_point_validates_before_launching():
     assert call(ldx=100) == nx.VXA_ERR_ARG
     assert call(x=None) == nx.VXA_ERR_ARG
     assert call(w=fake + 8) == nx.VXA_ERR_ARG
+
+
+def test_noalloc_entry_refuses_problems_beyond_its_scratch():
+    """vxa_exact_linear_op_noalloc checks its scratch need on the host and returns
+    VXA_ERR_TOO_LARGE before touching the device: 4096 rows of 4096 columns with a two-way
+    split over 4096 outputs needs 32 MiB of digits and 256 MiB of partials."""
+    L = nx.lib()
+    fake = ctypes.c_void_p(0x1000)
+    cfg = (ctypes.c_int32 * 7)(64, 64, 128, 4, 1, 8, 2)
+    rc = L.vxa_exact_linear_op_noalloc(fake, nx.VXA_BF16, 4096, fake, fake, fake, fake, nx.VXA_BF16, 4096, 4096,
+                                       4096, 4096, 14, 1, cfg, 7, None)
+    assert rc == nx.VXA_ERR_TOO_LARGE
+    assert b"scratch" in L.vxa_status_string(nx.VXA_ERR_TOO_LARGE)
+    with pytest.raises(ValueError, match="scratch"):
+        nx.check(rc, "exact_linear_op_noalloc")
+    # bad arguments are still refused first
+    assert L.vxa_exact_linear_op_noalloc(fake, nx.VXA_BF16, 64, fake, fake, fake, fake, nx.VXA_BF16, 64, 1, 64,
+                                         64, 16, 1, cfg, 7, None) == nx.VXA_ERR_ARG

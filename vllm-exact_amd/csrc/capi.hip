@@ -10,6 +10,7 @@ extern "C" const char* vxa_status_string(int status) {
     case VXA_ERR_UNSUPPORTED: return "unsupported shape or config";
     case VXA_ERR_WORKSPACE: return "workspace missing or too small";
     case VXA_ERR_LAUNCH: return "kernel launch failed";
+    case VXA_ERR_TOO_LARGE: return "problem larger than the fixed scratch of the no-allocation entry point";
     default: return "unknown status";
   }
 }

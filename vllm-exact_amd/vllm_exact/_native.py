@@ -7,6 +7,7 @@ argument types, and turns status codes into Python exceptions:
 * VXA_ERR_ARG         -> ValueError
 * VXA_ERR_UNSUPPORTED -> NotImplementedError (autotune and tuners skip such configs, as the
                          reference skips configs that fail, kernels.py:313-314)
+* VXA_ERR_TOO_LARGE   -> ValueError (a problem beyond vxa_exact_linear_op_noalloc's fixed scratch)
 * VXA_ERR_WORKSPACE / VXA_ERR_LAUNCH -> RuntimeError
 
 There is no fallback: if the library is missing, every GPU entry point raises.
@@ -19,7 +20,8 @@ import torch  # loads torch's HIP runtime first, so the library binds to that sa
 LIB_NAME = "libvllm_exact_amd.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
 
-VXA_OK, VXA_ERR_ARG, VXA_ERR_UNSUPPORTED, VXA_ERR_WORKSPACE, VXA_ERR_LAUNCH = range(5)
+VXA_OK, VXA_ERR_ARG, VXA_ERR_UNSUPPORTED, VXA_ERR_WORKSPACE, VXA_ERR_LAUNCH, VXA_ERR_TOO_LARGE = range(6)
+NOALLOC_SCRATCH_BYTES = 64 << 20  # VXA_NOALLOC_SCRATCH_BYTES
 VXA_F32, VXA_BF16, VXA_F16 = 0, 1, 2
 
 DTYPE_ENUM = {torch.float32: VXA_F32, torch.bfloat16: VXA_BF16, torch.float16: VXA_F16}
@@ -39,6 +41,7 @@ EXPORTED = (
     "vxa_paged_decode_workspace",
     "vxa_paged_decode",
     "vxa_paged_decode_prefix",
+    "vxa_exact_linear_op_noalloc",
 )
 
 _i64, _i32, _int, _vp, _sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
@@ -69,6 +72,11 @@ _SIGNATURES = {
         [_vp, _i64, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int, _vp],
     ),
     "vxa_paged_decode_workspace": (_int, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
+    "vxa_exact_linear_op_noalloc": (
+        _int,
+        [_vp, _int, _i64, _vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_i32), _int,
+         _vp],
+    ),
     "vxa_paged_decode": (
         _int,
         [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp,
@@ -122,7 +130,7 @@ def check(status, what):
     if status == VXA_OK:
         return
     msg = f"{what}: {lib().vxa_status_string(status).decode()} (status {status})"
-    if status == VXA_ERR_ARG:
+    if status in (VXA_ERR_ARG, VXA_ERR_TOO_LARGE):
         raise ValueError(msg)
     if status == VXA_ERR_UNSUPPORTED:
         raise NotImplementedError(msg)
