@@ -27,8 +27,18 @@ Also reported, from the same run:
   64/8K and 16/16K: ms per step as a HIP graph, the same step with hipBLASLt bf16 linears,
   bitwise batch invariance of the logits, and a CPU estimate from the oracle's timings;
 * bit-exactness of the benchmarked outputs against the CPU oracle (sampled rows);
-* `cpu_baseline`: the C oracle (OpenMP) on a bounded sample of the same sweep, extrapolated
-  per op, on this host's cores.
+* `per_op_f15`: the 4-dot variant, the same sweep at F = 15 (offset digits) with the table
+  tuned at F = 15, on weights packed at F = 15;
+* `config1`: M = 16, K = N = 4096, F = 14 with all four dots and no split-K: GEMM and op
+  times, and the whole fp32 and bf16 outputs checked bitwise against the oracle;
+* `cpu_baseline`: the reference's CPU path (the torch int64 statements digitize_torch +
+  exact_linear_torch) on every host thread (os.cpu_count() and torch.get_num_threads() are
+  printed), config 1 in full and a bounded sample of the sweep's weight rows extrapolated per
+  op; the C oracle (OpenMP) timed beside it as `oracle_c`.
+
+The roofline's `traffic` is the HBM bytes per launch measured by rocprofv3 FETCH_SIZE and
+WRITE_SIZE passes of `--profile-kernel` and recorded in profiles/; it is reported only when
+that record was made on a library built from the current sources (`traffic_source` says which).
 """
 import argparse
 import json
@@ -126,6 +136,190 @@ def gemm_ops(M, N, K, ndots=NDOTS):
     return ndots * 2 * M * N * K
 
 
+def time_op_and_gemm(torch, K, plugin, x, wc, N, Kd, F, trunc, cfg):
+    """Graph-replay times (us) of the full exactmm::linear op on weight copies wc, and of the
+    GEMM kernel it runs (the one-launch digitize + GEMM kernel where the table marks the row
+    count, else the GEMM on digits made beforehand). Returns (op_us, gemm_us, one_launch)."""
+    from vllm_exact.graph_timing import time_graph
+
+    M = x.shape[0]
+    nrot = len(wc)
+    t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
+    one_launch = plugin._one_launch(M, N, Kd)
+    if one_launch:
+        try:
+            K.exact_linear_bf16x(x, (wc[0][0], wc[0][2], wc[0][3]), Kd, F, trunc, cfg=cfg)
+        except NotImplementedError:
+            one_launch = False
+    if one_launch:
+        t_gemm = time_graph(lambda r: K.exact_linear_bf16x(x, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, trunc, cfg=cfg),
+                            nrot)
+    else:
+        xd = K.digitize_packed(x, F)
+        t_gemm = time_graph(lambda r: K.exact_linear_packed(xd, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, trunc,
+                                                            cfg=cfg), nrot)
+    return t_op, t_gemm, one_launch
+
+
+def roof_fields(M, N, Kd, t_us, ndots):
+    """GB/s, TOPS and roofline fractions of one exact GEMM launch of t_us microseconds."""
+    b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd, ndots)
+    t_roof = max(b / (HBM_PEAK_GBS * 1e9), o / (INT8_PEAK_TOPS * 1e12)) * 1e6
+    return dict(gemm_GBps=round(b / t_us / 1e3, 1), gemm_TOPS=round(o / t_us / 1e6, 1),
+                hbm_frac=round(b / t_us / 1e3 / HBM_PEAK_GBS, 3), mfma_frac=round(o / t_us / 1e6 / INT8_PEAK_TOPS, 3),
+                roofline_frac=round(t_roof / t_us, 3),
+                bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma")
+
+
+def sweep_f15(torch, K, plugin, weights, xs, table_f15, table_f14):
+    """The 4-dot variant: the sweep at F = 15 (offset digits, the reference's "f=15, 4 dots")
+    with the table tuned at F = 15, each op through exactmm::linear on weights packed at
+    F = 15, timed like the F = 14 sweep. Restores F = 14 and its table afterwards."""
+    from vllm_exact.graph_timing import rotations_for
+
+    recs = []
+    plugin.F, plugin.TRUNC = 15, False
+    plugin.load_table(table_f15)
+    try:
+        for name, N, Kd in SHAPES:
+            w = weights[name + ".bf16"]
+            wp = plugin.pack_weight(w)
+            wc = [wp] + [tuple(t.clone() for t in wp) for _ in range(max(3, rotations_for(2 * N * Kd)) - 1)]
+            for M in MS:
+                cfg = plugin._cfg(M, N, Kd)
+                t_op, t_gemm, one = time_op_and_gemm(torch, K, plugin, xs[(M, Kd)], wc, N, Kd, 15, False, cfg)
+                rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
+                           one_launch=one, **roof_fields(M, N, Kd, t_gemm, 4))
+                recs.append(rec)
+                log("f15", json.dumps(rec))
+            del wc, wp
+            torch.cuda.empty_cache()
+    finally:
+        plugin.F, plugin.TRUNC = F, TRUNC
+        plugin.load_table(table_f14)
+    return recs
+
+
+def config1(torch, K, plugin, oracle, np, dev, gen):
+    """The reference's CPU-runnable case on the GPU: M = 16, K = N = 4096, F = 14 with all four
+    dots, no split-K (the F = 14 table's cfg for the shape with SK = 1). The GEMM kernel and the
+    full op (digitize + GEMM) timed by graph replay over weight copies past the MALL; the whole
+    fp32 and bf16 outputs checked bitwise against the oracle."""
+    from vllm_exact.graph_timing import rotations_for, time_graph
+
+    M, N, Kd, Fc, trunc = 16, 4096, 4096, 14, False
+    cfg = tuple(plugin._cfg(M, N, Kd)[:6]) + (1,)
+    x = torch.randn(M, Kd, device=dev, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    wp = K.digitize_packed(w, Fc)
+    wc = [wp] + [tuple(t.clone() for t in wp) for _ in range(rotations_for(2 * N * Kd) - 1)]
+    xd = K.digitize_packed(x, Fc)
+    t_gemm = time_graph(lambda r: K.exact_linear_packed(xd, wc[r], Kd, Fc, trunc, cfg=cfg), len(wc))
+    t_two = time_graph(lambda r: K.exact_linear_packed(K.digitize_packed(x, Fc), wc[r], Kd, Fc, trunc, cfg=cfg),
+                       len(wc))
+    try:
+        t_one = time_graph(lambda r: K.exact_linear_bf16x(x, wc[r], Kd, Fc, trunc, cfg=cfg), len(wc))
+    except NotImplementedError:
+        t_one = None
+    y32 = K.exact_linear_packed(xd, wp, Kd, Fc, trunc, cfg=cfg).cpu().numpy()
+    yb = K.exact_linear_packed(xd, wp, Kd, Fc, trunc, cfg=cfg, out=torch.empty(M, N, device=dev,
+                                                                                dtype=torch.bfloat16))
+    ref = oracle.exact_linear_c(oracle.digitize_c(x.float().cpu().numpy(), Fc),
+                                oracle.digitize_c(w.float().cpu().numpy(), Fc), Fc, trunc)
+    exact = bool(np.array_equal(y32.view(np.uint32), ref.view(np.uint32))) and bool(np.array_equal(
+        yb.cpu().view(torch.int16).numpy().view(np.uint16), oracle.bf16_rne_c(ref).reshape(M, N)))
+    t_op = min(t for t in (t_two, t_one) if t is not None)
+    rec = dict(M=M, N=N, K=Kd, F=Fc, trunc=trunc, ndots=4, cfg=list(cfg), gemm_us=round(t_gemm, 2),
+               op_us=round(t_op, 2), op_two_launch_us=round(t_two, 2),
+               op_one_launch_us=None if t_one is None else round(t_one, 2), bit_exact_fp32_bf16=exact,
+               **roof_fields(M, N, Kd, t_gemm, 4))
+    log("config 1:", json.dumps(rec))
+    return rec
+
+
+def cpu_baseline_leg(torch, K, np, oracle, step_bytes, ops, budget_s):
+    """The reference's CPU path timed on this host: digitize_torch + exact_linear_torch, the
+    torch int64 statements of kernels.py:22-39, 89-100, on every host thread. Config 1
+    (16 x 4096 x 4096, 4 dots) runs in full; each sweep op runs on a sample of its weight rows
+    (rows are independent), its time extrapolated linearly in N (the activation digitize is
+    timed once, unscaled). Weights are digitized beforehand, as the reference does at load.
+    The C oracle (OpenMP) is timed beside it on the same sample budget."""
+    ncpu = os.cpu_count()
+    torch.set_num_threads(ncpu)
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(0)
+
+    def timed(fn, min_s):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            dt = (time.perf_counter() - t0) / reps
+            if reps * dt >= min_s or reps >= 1000:
+                return dt, reps
+
+    # config 1 in full
+    x1 = torch.randn(16, 4096, generator=g).to(torch.bfloat16).float()
+    w1 = (torch.randn(4096, 4096, generator=g) * 0.02).to(torch.bfloat16).float()
+    wd1 = K.digitize_torch(w1, 14)
+    t1, r1 = timed(lambda: K.exact_linear_torch(K.digitize_torch(x1, 14), wd1, 14, trunc=False), 1.0)
+    c1 = dict(seconds=round(t1, 4), GBps=round(gemm_bytes(16, 4096, 4096) / t1 / 1e9, 3),
+              GOPs=round(gemm_ops(16, 4096, 4096, 4) / t1 / 1e9, 3), reps=r1, sample="full (not extrapolated)")
+
+    # the sweep: sampled weight rows per op
+    per_op_s = budget_s / len(ops)
+    # at most 2048 weight rows a shape are sampled
+    wfull = {name: (torch.randn(min(N, 2048), Kd, generator=g) * 0.02).to(torch.bfloat16).float()
+             for name, N, Kd in SHAPES}
+    total_s, desc, op_s = 0.0, [], {}
+    for M, name, N, Kd in ops:
+        x = torch.randn(M, Kd, generator=g).to(torch.bfloat16).float()
+        t_dig, _ = timed(lambda: K.digitize_torch(x, F), 0.05)
+        xd = K.digitize_torch(x, F)
+        # calibrate on 64 weight rows, then one timed sample sized to the op's share of the budget
+        wd = K.digitize_torch(wfull[name][:64], F)
+        t0 = time.perf_counter()
+        K.exact_linear_torch(xd, wd, F, TRUNC)
+        per_row = (time.perf_counter() - t0) / 64
+        ns = int(min(N, 2048, max(64, per_op_s / max(per_row, 1e-9)))) // 16 * 16
+        wd = K.digitize_torch(wfull[name][:ns], F)
+        t0 = time.perf_counter()
+        K.exact_linear_torch(xd, wd, F, TRUNC)
+        t_lin, reps = time.perf_counter() - t0, 1
+        t = t_dig + t_lin * N / ns
+        op_s[(M, name)] = t
+        total_s += t
+        desc.append(f"M={M} {name} {ns}/{N} rows x{reps}")
+    cpu = dict(value=round(step_bytes / total_s / 1e9, 4), unit="GB/s", cores=threads, kind="port",
+               os_cpu_count=ncpu, torch_threads=threads,
+               sample="torch int64 statements of the reference's CPU path (kernels.digitize_torch + "
+                      "kernels.exact_linear_torch) on every host thread; each sweep op on its first weight rows, "
+                      "time extrapolated linearly in N (labelled extrapolated); config 1 in full: "
+                      + "; ".join(desc),
+               step_ms_extrapolated=round(total_s * 1e3, 1), config1_full=c1)
+
+    # the C oracle on the same kind of sample
+    rng = np.random.default_rng(0)
+    samples = {}
+    for name, N, Kd in SHAPES:
+        ns = min(N, 2048)
+        samples[name] = (ns, oracle.digitize_c((rng.standard_normal((ns, Kd)) * 0.02).astype(np.float32), F))
+    oc_total, oc_desc, oc_op = 0.0, [], {}
+    for M, name, N, Kd in ops:
+        ns, wd = samples[name]
+        x = rng.standard_normal((M, Kd)).astype(np.float32)
+        dt, reps = timed(lambda: oracle.exact_linear_c(oracle.digitize_c(x, F), wd, F, TRUNC), per_op_s / 3)
+        oc_op[(M, name)] = dt * N / ns
+        oc_total += dt * N / ns
+        oc_desc.append(f"M={M} {name} {ns}/{N} rows x{reps}")
+    cpu["oracle_c"] = dict(value=round(step_bytes / oc_total / 1e9, 3), unit="GB/s", cores=oracle.cpu_threads(),
+                           step_ms_extrapolated=round(oc_total * 1e3, 1),
+                           sample="C oracle (digitize + exact integer digit dots, OpenMP), time extrapolated "
+                                  "linearly in N: " + "; ".join(oc_desc))
+    log("cpu baseline:", json.dumps(cpu))
+    return cpu, op_s
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +332,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--table", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F14.json"),
                     help="exact_int8 tuning table to use")
+    ap.add_argument("--table-f15", default=str(ROOT / "vllm-exact_amd" / "vllm_exact" / "cfg_table_mi355x_F15.json"),
+                    help="tuning table of the 4-dot F = 15 sweep (per_op_f15)")
+    ap.add_argument("--no-f15", action="store_true", help="skip the 4-dot F = 15 sweep and the config-1 timing")
     ap.add_argument("--profile-counters", action="store_true",
                     help="only launch every sweep GEMM (table cfg, weights rotated past the MALL) and the three "
                          "decode-attention shapes, 5 times each, then a 1 GiB copy: the program rocprofv3 --pmc "
@@ -151,12 +348,28 @@ def parse():
 TRAFFIC_SUMMARY = ROOT / "profiles" / "exact_gemm_m256_gate_up_hbm_traffic.md"
 
 
+def kernel_sources_sha16():
+    """Hash of every source the HIP library is built from (its csrc/ files and the C header):
+    a traffic figure measured on one build is only reported for a library built from the
+    same sources."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted((ROOT / "vllm-exact_amd" / "csrc").glob("*")) + [ROOT / "include" / "vllm_exact_amd.h"]
+    for f in files:
+        if f.is_file():
+            h.update(f.name.encode() + b"\0" + f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def read_traffic(kernel_cfg):
     """HBM bytes per launch of the dominant GEMM, as measured by the rocprofv3 FETCH_SIZE and
     WRITE_SIZE passes of `bench.py --profile-kernel` and recorded in TRAFFIC_SUMMARY (its
-    `traffic_bytes_per_launch` and `cfg` lines); None when no measurement matches this cfg."""
+    `traffic_bytes_per_launch`, `cfg` and `kernel_sources_sha16` lines). Returns (bytes,
+    where the figure comes from), or (None, why not) when the summary was measured with
+    another cfg or on a library built from other sources."""
     if not TRAFFIC_SUMMARY.exists():
-        return None
+        return None, "no traffic summary"
     vals = {}
     for line in TRAFFIC_SUMMARY.read_text().splitlines():
         if line.startswith("    ") and "=" in line:
@@ -164,10 +377,14 @@ def read_traffic(kernel_cfg):
             vals[k.strip()] = v.strip()
     try:
         if json.loads(vals["cfg"]) != list(kernel_cfg):
-            return None
-        return int(vals["traffic_bytes_per_launch"])
+            return None, f"{TRAFFIC_SUMMARY.name} was measured with cfg {vals['cfg']}"
+        if vals.get("kernel_sources_sha16") != kernel_sources_sha16():
+            return None, f"{TRAFFIC_SUMMARY.name} was measured on a library built from other sources"
+        return int(vals["traffic_bytes_per_launch"]), (
+            f"profiles/{TRAFFIC_SUMMARY.name}: rocprofv3 FETCH_SIZE + WRITE_SIZE of bench.py --profile-kernel on "
+            f"this library's sources (sha16 {vals['kernel_sources_sha16']}), calibrated on a 1 GiB copy")
     except (KeyError, ValueError):
-        return None
+        return None, f"{TRAFFIC_SUMMARY.name} is incomplete"
 
 
 def profile_kernel(args):
@@ -205,7 +422,8 @@ def profile_kernel(args):
     torch.cuda.synchronize()
     print(json.dumps({"gemm": f"M={M} {name} {N}x{Kd}", "cfg": list(cfg), "launches": args.steps,
                       "weight_copies": rot, "copy_bytes": src.numel() * 2,
-                      "algorithmic_bytes": gemm_bytes(M, N, Kd)}), flush=True)
+                      "algorithmic_bytes": gemm_bytes(M, N, Kd), "kernel_sources_sha16": kernel_sources_sha16()}),
+          flush=True)
 
 
 def profile_counters(args):
@@ -374,22 +592,7 @@ def main():
         for M in MS:
             cfg = plugin._cfg(M, N, Kd)
             x = xs[(M, Kd)]
-            xd = K.digitize_packed(x, F)
-            t_op = time_graph(lambda r: torch.ops.exactmm.linear(x, *wc[r]), nrot)
-            # the GEMM kernel the op runs: where the table marks the row count, the one-launch
-            # digitize + GEMM kernel (x read as bf16), otherwise the GEMM on digits digitized beforehand
-            one_launch = plugin._one_launch(M, N, Kd)
-            if one_launch:
-                try:
-                    K.exact_linear_bf16x(x, (wc[0][0], wc[0][2], wc[0][3]), Kd, F, TRUNC, cfg=cfg)
-                except NotImplementedError:
-                    one_launch = False
-            if one_launch:
-                t_gemm = time_graph(lambda r: K.exact_linear_bf16x(x, (wc[r][0], wc[r][2], wc[r][3]), Kd, F, TRUNC,
-                                                                   cfg=cfg), nrot)
-            else:
-                t_gemm = time_graph(lambda r: K.exact_linear_packed(xd, (wc[r][0], wc[r][2], wc[r][3]), Kd, F,
-                                                                    TRUNC, cfg=cfg), nrot)
+            t_op, t_gemm, one_launch = time_op_and_gemm(torch, K, plugin, x, wc, N, Kd, F, TRUNC, cfg)
             t_bf16 = time_graph(lambda r: torch.matmul(x, wbs[r].T), len(wbs))
             t_i8 = None
             if M > 16:
@@ -398,14 +601,9 @@ def main():
                     t_i8 = round(time_graph(lambda r: torch._int_mm(a8, b8[r].T), len(b8)), 2)
                 except RuntimeError:
                     t_i8 = None
-            b, o = gemm_bytes(M, N, Kd), gemm_ops(M, N, Kd)
-            t_roof = max(b / (HBM_PEAK_GBS * 1e9), o / (INT8_PEAK_TOPS * 1e12)) * 1e6
             rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
                        bf16_hipblaslt_us=round(t_bf16, 2), int8_1dot_vendor_us=t_i8,
-                       gemm_GBps=round(b / t_gemm / 1e3, 1),
-                       gemm_TOPS=round(o / t_gemm / 1e6, 1), hbm_frac=round(b / t_gemm / 1e3 / HBM_PEAK_GBS, 3),
-                       mfma_frac=round(o / t_gemm / 1e6 / INT8_PEAK_TOPS, 3), roofline_frac=round(t_roof / t_gemm, 3),
-                       bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma",
+                       **roof_fields(M, N, Kd, t_gemm, NDOTS),
                        vs_bf16=round(t_op / t_bf16, 2), weight_copies=nrot, one_launch=one_launch)
             per_op[(M, name)] = rec
             log(json.dumps(rec))
@@ -434,7 +632,8 @@ def main():
     else:
         roof = dict(bound="mfma", achieved=round(o / t_kernel / 1e6, 1), peak=INT8_PEAK_TOPS, unit="TFLOP/s",
                     frac=round(o / t_kernel / 1e6 / INT8_PEAK_TOPS, 4), traffic=None)
-    roof["traffic"] = read_traffic(cfg) if (M, name) == (256, "gate_up") else None
+    roof["traffic"], roof["traffic_source"] = (read_traffic(cfg) if (M, name) == (256, "gate_up")
+                                               else (None, "no traffic measurement for this kernel"))
     roof.update(kernel=f"exact GEMM M={M} {name} {N}x{Kd} cfg={list(cfg)}", kernel_us=round(t_kernel, 2),
                 algorithmic_bytes=b, algorithmic_ops=o)
     log("roofline:", json.dumps(roof))
@@ -454,6 +653,12 @@ def main():
         got = torch.from_numpy(y[rows]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
         exact_ok &= bool(np.array_equal(got, want))
     log("bit-exact vs oracle:", exact_ok)
+
+    # ---------------------------------------------------------------- 4 dots: F = 15 sweep, config 1
+    per_op_f15, cfg1 = [], None
+    if not args.no_f15:
+        per_op_f15 = sweep_f15(torch, K, plugin, weights, xs, args.table_f15, args.table)
+        cfg1 = config1(torch, K, plugin, oracle, np, dev, gen)
 
     # ---------------------------------------------------------------- attention
     attn = []
@@ -566,40 +771,16 @@ def main():
         del model
         torch.cuda.empty_cache()
 
-    # ---------------------------------------------------------------- CPU baseline (oracle, sampled)
+    # ---------------------------------------------------------------- CPU baseline (reference CPU path, sampled)
     cpu = None
     if not args.no_cpu:
-        threads = oracle.cpu_threads()
-        rng = np.random.default_rng(0)
-        samples = {}
-        for name, N, Kd in SHAPES:
-            ns = min(N, 2048)
-            w = (rng.standard_normal((ns, Kd)) * 0.02).astype(np.float32)
-            samples[name] = (ns, oracle.digitize_c(w, F))
-        total_s, sample_desc, cpu_op_s = 0.0, [], {}
-        min_s = args.cpu_seconds / len(ops)
-        for M, name, N, Kd in ops:
-            ns, wd = samples[name]
-            x = rng.standard_normal((M, Kd)).astype(np.float32)
-            reps, t0 = 0, time.perf_counter()
-            while True:
-                xdn = oracle.digitize_c(x, F)
-                oracle.exact_linear_c(xdn, wd, F, TRUNC)
-                reps += 1
-                dt = (time.perf_counter() - t0) / reps
-                if reps * dt >= min_s or reps >= 5000:
-                    break
-            total_s += dt * N / ns
-            cpu_op_s[(M, name)] = dt * N / ns
-            sample_desc.append(f"M={M} {name} {ns}/{N} rows x{reps}")
-        cpu = dict(value=round(step_bytes / total_s / 1e9, 3), unit="GB/s", cores=threads, kind="port",
-                   sample="C oracle (digitize + exact integer digit dots, OpenMP) on the first rows of every op "
-                          "of the sweep, time extrapolated linearly in N: " + "; ".join(sample_desc),
-                   step_ms_extrapolated=round(total_s * 1e3, 1))
-        log("cpu baseline:", json.dumps(cpu))
+        del weights
+        torch.cuda.empty_cache()
+        cpu, cpu_op_s = cpu_baseline_leg(torch, K, np, oracle, step_bytes, ops, args.cpu_seconds)
         if decode:
-            # decode step on the CPU, extrapolated: the sampled per-op linear times at M = B,
+            # decode step on the CPU, extrapolated: the sampled per-op torch times at M = B,
             # lm_head scaled from QKV by N, attention from a timed fp64 oracle sample
+            rng = np.random.default_rng(1)
             Ls = 1024
             qs = rng.standard_normal((1, ATT_H, ATT_D)).astype(np.float32)
             cache = rng.standard_normal((Ls // ATT_BS, ATT_BS, ATT_KV, ATT_D)).astype(np.float32)
@@ -639,6 +820,8 @@ def main():
         "cpu_baseline": cpu,
         "bit_exact": exact_ok,
         "per_op": per_op,
+        "per_op_f15": per_op_f15,
+        "config1": cfg1,
         "attention": attn,
         "lm_head": lm_head,
         "decode_step": decode,

@@ -97,23 +97,32 @@ def test_shipped_table_is_well_formed(path):
                 assert (cfg[0], cfg[1], cfg[4], cfg[3]) in xw, cfg
 
 
-def test_bench_traffic_summary_matches_the_table():
+def test_bench_traffic_is_tied_to_cfg_and_sources(tmp_path, monkeypatch):
     # bench.py reports roofline.traffic from the rocprofv3 FETCH/WRITE summary only when it
-    # was measured with the cfg the table now gives the dominant GEMM (M = 256 gate_up)
+    # was measured with the dominant GEMM's cfg on a library built from the current sources
     import importlib.util
     from pathlib import Path
     root = Path(__file__).resolve().parents[1]
     spec = importlib.util.spec_from_file_location("bench_mod", root / "bench.py")
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    plugin.load_table(vllm_exact.TABLES["mi355x"])
-    try:
-        cfg = plugin._cfg(256, 24576, 4096)
-    finally:
-        plugin.load_table(None)
-    traffic = bench.read_traffic(cfg)
-    assert traffic is not None and traffic > bench.gemm_bytes(256, 24576, 4096)
-    assert bench.read_traffic((1, 2, 3, 4, 5, 6, 7)) is None
+    sha = bench.kernel_sources_sha16()
+    assert len(sha) == 16 and sha == bench.kernel_sources_sha16()
+    summary = tmp_path / "traffic.md"
+    monkeypatch.setattr(bench, "TRAFFIC_SUMMARY", summary)
+    cfg = (128, 192, 64, 8, 3, 8, 1)
+
+    def write(cfg_, sha_):
+        summary.write_text(f"# traffic\n\n    cfg = {list(cfg_)}\n    traffic_bytes_per_launch = 231361984\n"
+                           f"    kernel_sources_sha16 = {sha_}\n")
+
+    write(cfg, sha)
+    traffic, src = bench.read_traffic(cfg)
+    assert traffic == 231361984 and sha in src
+    assert bench.read_traffic((1, 2, 3, 4, 5, 6, 7))[0] is None
+    write(cfg, "0" * 16)
+    traffic, why = bench.read_traffic(cfg)
+    assert traffic is None and "other sources" in why
 
 
 def test_bench_refuses_more_than_one_gpu():
