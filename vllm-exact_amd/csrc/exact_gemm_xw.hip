@@ -18,6 +18,10 @@
 // Every step issues the same loads (past the last step they repeat step nk-1 into a stage or
 // set no live step reads), so the wait count is one constant and the loop has no branch.
 //
+// Epilogue: for 2-byte outputs without a K split or offset terms (the STAGED instantiations)
+// the workgroup converts its accumulators, assembles the BM x BN tile in the free x ring and
+// stores it as 16-byte pieces of whole rows; otherwise every lane stores its own values.
+//
 // Products and sums are the same int32 MFMA dot products as the other kernels; only the
 // order of integer additions differs, which changes no bit.
 
@@ -32,7 +36,15 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int BM, int NWN, int WN, int R, int WMS, bool TRUNC>
+// Bytes of one row of the output tile as the epilogue stages it in LDS: BN 2-byte values plus
+// 16 bytes of padding, so the four row groups of one LDS store land on different banks
+// (BN is a multiple of 32).
+constexpr int staged_row_bytes(int bn) { return bn * 2 + 16; }
+// The staged tile fits in the x ring.
+constexpr bool staged_fits(int bm, int bn, int r) { return bm * staged_row_bytes(bn) <= (r + 1) * 2 * (bm / 16) * 1024; }
+
+// STAGED: 2-byte output, one K split, no F = 15 offset terms; the epilogue goes through LDS.
+template <int BM, int NWN, int WN, int R, int WMS, bool TRUNC, bool STAGED>
 __global__ __launch_bounds__(64 * NWN * WMS) void exact_xw_kernel(ExactParams p) {
   constexpr int NWAVE = NWN * WMS;  // waves: NWN along N times WMS along M
   constexpr int TMA = BM / 16;      // 16-row tiles of the x tile
@@ -46,6 +58,7 @@ __global__ __launch_bounds__(64 * NWN * WMS) void exact_xw_kernel(ExactParams p)
   constexpr int kWait = (R - 1) * (LX + LW);
   static_assert(TMA % WMS == 0, "row tiles split evenly over the waves along M");
   static_assert(kWait <= 63, "vmcnt limit");
+  static_assert(!STAGED || staged_fits(BM, BN, R), "staged tile fits the ring");
   __shared__ __attribute__((aligned(1024))) int8_t ring[S * NFX * 1024];
 
   const int lane = threadIdx.x & 63;
@@ -131,6 +144,24 @@ __global__ __launch_bounds__(64 * NWN * WMS) void exact_xw_kernel(ExactParams p)
       ll[tm][tn] = v4i{0, 0, 0, 0};
     }
 
+  // Row and column scales of this wave's outputs, loaded before the K loop so the staged
+  // epilogue does not wait for them, where the registers allow: accumulators, weight ring and
+  // x fragments (VGPRs of one wave) plus the scales stay 32 below the budget of a wave, 256
+  // registers when two or more waves share a SIMD and 512 (with the accumulation registers)
+  // when one does.
+  const int r16 = lane & 15, kq = lane >> 4;
+  constexpr int kLiveRegs = 4 * (TM * TN * (TRUNC ? 2 : 3) + R * LW + 2 * TM) + 4 * TM + TN;
+  constexpr bool kPrefetch = STAGED && kLiveRegs <= (NWAVE > 4 ? 224 : 480);
+  int32_t swp[TN], sxp[TM][4];
+  if constexpr (kPrefetch) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) swp[tn] = p.sw[min(n0 + tn * 16 + r16, p.N - 1)];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sxp[tm][r] = p.sx[min(m0 + tm * 16 + kq * 4 + r, p.M - 1)];
+  }
+
   const int8_t* lds_lane = ring + lane * 16;
   auto step = [&](int64_t j, v4i (&wb)[LW]) {
     // lgkmcnt(0): this wave's reads of stage j-1 are complete before any wave refills it
@@ -187,8 +218,48 @@ __global__ __launch_bounds__(64 * NWN * WMS) void exact_xw_kernel(ExactParams p)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  // Epilogue from registers: register r of lane holds C[4*(lane>>4) + r][lane & 15].
-  const int r16 = lane & 15, kq = lane >> 4;
+  // Register r of lane holds C[4*(lane>>4) + r][lane & 15] of each 16 x 16 tile: a store
+  // straight from registers writes 2-byte values 16 to a row. The staged epilogue first
+  // assembles the workgroup's BM x BN tile in LDS (the x ring is free now), then writes it
+  // out in 16-byte pieces, whole rows at a time.
+  if constexpr (STAGED) {
+    constexpr int kRowBytes = staged_row_bytes(BN);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = min(m0 + tm * 16 + kq * 4 + r, p.M - 1);
+        const int32_t sxm = kPrefetch ? sxp[tm][r] : p.sx[m];
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+          const int64_t n = min(n0 + tn * 16 + r16, p.N - 1);
+          int64_t tot = ((int64_t)hh[tm][tn][r] << 16) + ((int64_t)md[tm][tn][r] << 8);
+          if constexpr (!TRUNC) tot += (int64_t)ll[tm][tn][r];
+          const float v = exact_epilogue(tot, sxm, kPrefetch ? swp[tn] : p.sw[n]);
+          const uint16_t bits = p.out_dtype == VXA_BF16 ? f32_to_bf16_rne(v) : __builtin_bit_cast(uint16_t, (_Float16)v);
+          const int row = wm * (BM / WMS) + tm * 16 + kq * 4 + r;
+          const int col = wn * WN + tn * 16 + r16;
+          *reinterpret_cast<uint16_t*>(ring + row * kRowBytes + col * 2) = bits;
+        }
+      }
+    __syncthreads();
+    constexpr int kPieces = BN / 8;  // 16-byte pieces per row
+    const bool whole = reinterpret_cast<uintptr_t>(p.out) % 16 == 0 && p.ldo % 8 == 0;
+    for (int i = threadIdx.x; i < BM * kPieces; i += 64 * NWAVE) {
+      const int row = i / kPieces, c = i % kPieces;
+      const int64_t m = bm * BM + row, n = bn * BN + c * 8;
+      if (m >= p.M || n >= p.N) continue;
+      const int8_t* src = ring + row * kRowBytes + c * 16;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + m * p.ldo + n;
+      if (whole && n + 8 <= p.N) {
+        *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
+      } else {
+        for (int e = 0; e < 8 && n + e < p.N; ++e) dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
@@ -207,10 +278,17 @@ __global__ __launch_bounds__(64 * NWN * WMS) void exact_xw_kernel(ExactParams p)
 
 template <int BM, int NWN, int WN, int R, int WMS, bool TRUNC>
 hipError_t launch(const ExactParams& ep, hipStream_t st) {
+  constexpr bool kCanStage = staged_fits(BM, NWN * WN, R);
   const int64_t blocks = cdiv<int64_t>(ep.M, BM) * cdiv<int64_t>(ep.N, NWN * WN);
   if (blocks > 0x7FFFFFFFLL || ep.sk > 65535) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((exact_xw_kernel<BM, NWN, WN, R, WMS, TRUNC>), dim3((unsigned)blocks, (unsigned)ep.sk),
-                     dim3(64 * NWN * WMS), 0, st, ep);
+  const dim3 grid((unsigned)blocks, (unsigned)ep.sk), block(64 * NWN * WMS);
+  if constexpr (kCanStage) {
+    if (ep.sk == 1 && ep.out_dtype != VXA_F32 && !ep.offset) {
+      hipLaunchKernelGGL((exact_xw_kernel<BM, NWN, WN, R, WMS, TRUNC, true>), grid, block, 0, st, ep);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((exact_xw_kernel<BM, NWN, WN, R, WMS, TRUNC, false>), grid, block, 0, st, ep);
   return hipGetLastError();
 }
 
