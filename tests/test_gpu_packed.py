@@ -65,6 +65,30 @@ def test_packed_gemm_bitwise(F, tr, M, N, Kd):
     assert np.array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), want_b)
 
 
+@pytest.mark.parametrize("tr", [True, False])
+def test_xw_two_byte_outputs_every_tile(tr):
+    """The x-through-LDS kernels write a 2-byte output without a K split through an LDS-staged
+    tile and 16-byte row pieces. Every tile shape, at ragged M, N and K: bf16 into a view
+    whose row stride is a multiple of 8 (whole pieces, then an element-wise tail: 203 columns)
+    and fp16 into a contiguous 203-column tensor (row starts not 16-byte aligned: every piece
+    element-wise), both equal to the oracle's fp32 rounded once to nearest even."""
+    M, N, Kd, F = 70, 203, 1000, 14
+    x, w = stress_xw(M, N, Kd, seed=7)
+    xd, wd = K.digitize(x.to(DEV), F), K.digitize(w.to(DEV), F)
+    ref = oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr)
+    want_b = oracle.bf16_rne_c(ref).reshape(M, N)
+    want_h = ref.astype(np.float16).view(np.uint16)
+    xp, wp = K.pack_digits(xd), K.pack_digits(wd)
+    for bm, bn, r, nw in K.XW_SHAPES:
+        cfg = (bm, bn, 64, nw, r, 8, 1)
+        yb = torch.full((M, N + 5), -1.0, device=DEV, dtype=torch.bfloat16)[:, :N]  # row stride 208
+        K.exact_linear_packed(xp, wp, Kd, F, tr, out=yb, cfg=cfg)
+        assert np.array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), want_b), ("bf16", cfg)
+        yh = torch.empty(M, N, device=DEV, dtype=torch.float16)
+        K.exact_linear_packed(xp, wp, Kd, F, tr, out=yh, cfg=cfg)
+        assert np.array_equal(yh.cpu().numpy().view(np.uint16), want_h), ("fp16", cfg)
+
+
 FUSED_CFGS = tuple((16, 16 * nt, 128, nwk, c, 8, 1) for mt, nt, c, nwk in K.SMALL_SHAPES if mt == 1)
 
 
