@@ -341,6 +341,11 @@ def parse():
                     help="only launch every sweep GEMM (table cfg, weights rotated past the MALL) and the three "
                          "decode-attention shapes, 5 times each, then a 1 GiB copy: the program rocprofv3 --pmc "
                          "passes (MFMA utilisation, FETCH_SIZE, WRITE_SIZE) run; one JSON line per launch group")
+    ap.add_argument("--floors", action="store_true",
+                    help="only measure the achievable ceilings of the paths the kernels run on (vllm-exact_amd/floors): "
+                         "MFMA issue rate, LDS read rate, L2-resident load rate into VGPRs and straight into LDS, "
+                         "streaming reads at the sweep's weight sizes (graph replay, buffers rotated past the MALL) "
+                         "and reads of permuted 8 KiB pages; one JSON line")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch the dominant GEMM (M=256 gate_up, table cfg) and a 1 GiB copy, --steps times "
                          "each: the program rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs to measure HBM traffic")
@@ -491,6 +496,159 @@ def profile_counters(args):
     torch.cuda.synchronize()
     print(json.dumps({"group": "copy", "launches": 3, "bytes": src.numel() * 2}), flush=True)
 
+FLOORS_LIB = ROOT / "vllm-exact_amd" / "vllm_exact" / "libvxa_floors.so"
+FLOORS_SRC = ROOT / "vllm-exact_amd" / "floors" / "floors.hip"
+
+
+def floors(args):
+    """Achievable ceilings of the paths the exact GEMM and the attention run on, measured with
+    the probe kernels of vllm-exact_amd/floors/floors.hip (which compute nothing useful). Each
+    kernel-timed figure is one launch timed with HIP events on torch's stream; the streaming
+    reads at the sweep's weight sizes are timed like the GEMMs (graph replay, buffers rotated
+    past the MALL). The shader clock comes from s_memtime cycles over event time."""
+    import ctypes
+    import hashlib
+    import statistics
+
+    import torch
+
+    from vllm_exact.graph_timing import rotations_for, time_graph
+
+    lib = ctypes.CDLL(str(FLOORS_LIB))
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.vxf_stream.argtypes = [vp, i64, i64, i32, i32, i32, vp, vp, vp]
+    lib.vxf_pages.argtypes = [vp, i64, vp, i32, i32, i32, vp, vp, vp]
+    lib.vxf_l2.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp, vp]
+    lib.vxf_lds.argtypes = [i32, i32, i32, vp, vp, vp]
+    lib.vxf_mfma.argtypes = [i32, i32, i32, vp, vp, vp]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    max_blocks = 4096
+    sink = torch.zeros(max_blocks * 1024, device=dev, dtype=torch.int32)
+    cyc = torch.zeros(max_blocks, device=dev, dtype=torch.int64)
+
+    def st():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"floors probe refused its arguments or failed to launch (status {rc})")
+
+    def timed(launch, blocks, reps=5):
+        """Median event time (us) of one launch and the mean shader cycles of its workgroups."""
+        assert blocks <= max_blocks
+        launch()
+        torch.cuda.synchronize()
+        us, cycles = [], []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            launch()
+            b.record()
+            b.synchronize()
+            us.append(a.elapsed_time(b) * 1000.0)
+            cycles.append(cyc[:blocks].double().mean().item())
+        return statistics.median(us), statistics.median(cycles)
+
+    out = {"mode": "floors", "cus": ncu, "source_sha16": hashlib.sha256(FLOORS_SRC.read_bytes()).hexdigest()[:16]}
+
+    # MFMA issue rate: 8 independent v_mfma_i32_16x16x64_i8 chains per wave, one workgroup per CU
+    mf = []
+    for waves in (4, 8, 16):
+        rounds = 4096
+        us, cy = timed(lambda: check(lib.vxf_mfma(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())), ncu)
+        per_simd = rounds * 8 * waves / 4
+        ops = ncu * waves * rounds * 8 * 16 * 16 * 64 * 2
+        mf.append({"waves_per_cu": waves, "us": round(us, 1), "ghz": round(cy / us / 1e3, 3),
+                   "cycles_per_mfma_per_simd": round(cy / per_simd, 2), "TOPS": round(ops / us / 1e6, 1)})
+        log("mfma", mf[-1])
+    out["mfma_i8_16x16x64"] = mf
+    ghz = statistics.median(r["ghz"] for r in mf)
+
+    # LDS reads: ds_read_b128, 8 in flight per lane
+    ld = []
+    for waves in (4, 8, 16):
+        rounds = 2048
+        us, cy = timed(lambda: check(lib.vxf_lds(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())), ncu)
+        b = rounds * 8 * 64 * 16 * waves
+        ld.append({"waves_per_cu": waves, "us": round(us, 1), "bytes_per_clk_per_cu": round(b / cy, 1)})
+        log("lds", ld[-1])
+    out["lds_read_b128"] = ld
+
+    # L2-resident loads (2 MiB buffer: every XCD's L2 holds it), into VGPRs or straight into LDS
+    l2buf = torch.zeros(1 << 21, device=dev, dtype=torch.uint8)
+    l2 = []
+    for lds in (0, 1):
+        for waves in (4, 8, 16):
+            for q in (1, 2, 4, 8):
+                rounds = max(64, 16384 // (q * waves))
+                us, cy = timed(lambda: check(lib.vxf_l2(l2buf.data_ptr(), l2buf.numel(), lds, q, waves, ncu, rounds,
+                                                        sink.data_ptr(), cyc.data_ptr(), st())), ncu)
+                b = rounds * q * 1024 * waves
+                l2.append({"path": "lds" if lds else "vgpr", "waves_per_cu": waves, "loads_in_flight": q,
+                           "us": round(us, 1), "bytes_per_clk_per_cu": round(b / cy, 1),
+                           "TBps": round(b * ncu / us / 1e6, 2)})
+                log("l2", l2[-1])
+    out["l2_load_16B"] = l2
+    del l2buf
+
+    # Streaming reads at the sweep's weight sizes, timed like the GEMMs
+    sizes = {"o": 4096 * 4096 * 2, "qkv": 6144 * 4096 * 2, "down": 4096 * 12288 * 2, "gate_up": 24576 * 4096 * 2}
+    stream_rows = []
+    for name, nbytes in sizes.items():
+        rot = rotations_for(nbytes)
+        bufs = [torch.empty(nbytes, device=dev, dtype=torch.uint8) for _ in range(rot)]
+        best = None
+        for blocks in (256, 512, 1024):
+            for q in (4, 8):
+                per_wg = nbytes // blocks
+                per_wg -= per_wg % (16 * 512 * q)
+                if per_wg <= 0:
+                    continue
+
+                def call(i, blocks=blocks, q=q, per_wg=per_wg):
+                    check(lib.vxf_stream(bufs[i].data_ptr(), nbytes, per_wg, blocks, 512, q, sink.data_ptr(),
+                                         cyc.data_ptr(), st()))
+
+                us = time_graph(call, rotations=rot)
+                row = {"blocks": blocks, "loads_in_flight": q, "us": round(us, 2),
+                       "bytes_read": per_wg * blocks, "hbm_frac": round(per_wg * blocks / us / 1e6 / HBM_PEAK_GBS, 3)}
+                if best is None or row["us"] < best["us"]:
+                    best = row
+        stream_rows.append({"weights_of": name, "bytes": nbytes, "copies": rot, **best})
+        log("stream", stream_rows[-1])
+        del bufs
+        torch.cuda.empty_cache()
+    empty_us = time_graph(lambda i: check(lib.vxf_mfma(4, 1, 1, sink.data_ptr(), cyc.data_ptr(), st())))
+    out["stream_read"] = stream_rows
+    out["empty_launch_us"] = round(empty_us, 2)
+
+    # Permuted 8 KiB pages (the paged KV stream): 1 GiB, each page read once
+    nb = 1 << 30
+    pbuf = torch.empty(nb, device=dev, dtype=torch.uint8)
+    npg = nb // 8192
+    gen = torch.Generator(device=dev).manual_seed(0)
+    perm = torch.randperm(npg, device=dev, generator=gen).to(torch.int32)
+    assert int(perm.max()) < npg and int(perm.min()) >= 0
+    pg = []
+    for blocks in (1024, 2048, 4096):
+        ppw = npg // blocks
+        for q in (1, 2, 4):
+            us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, q,
+                                                      sink.data_ptr(), cyc.data_ptr(), st())), blocks)
+            pg.append({"blocks": blocks, "pages_in_flight": q, "us": round(us, 1),
+                       "TBps": round(blocks * ppw * 8192 / us / 1e6, 2)})
+            log("pages", pg[-1])
+    out["permuted_8k_pages"] = pg
+    seq = torch.arange(npg, device=dev, dtype=torch.int32)
+    us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, seq.data_ptr(), 2048, npg // 2048, 2,
+                                              sink.data_ptr(), cyc.data_ptr(), st())), 2048)
+    out["sequential_8k_pages_TBps"] = round(nb / us / 1e6, 2)
+    out["ghz_under_mfma"] = ghz
+    print(json.dumps(out), flush=True)
+
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -507,6 +665,9 @@ def main():
         return
     if args.profile_counters:
         profile_counters(args)
+        return
+    if args.floors:
+        floors(args)
         return
     import numpy as np
     import torch

@@ -3,7 +3,8 @@
 The packed layout has no counterpart in the reference; tests/helpers.pack_np states it
 independently in numpy. Checks: GPU packing matches it byte for byte; digitize_packed equals
 pack(digitize) and the oracle's digits; the packed GEMM equals the oracle bitwise for every
-kernel family (small-M, LDS ring, x through LDS with weights in registers), ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
+kernel family (small-M, LDS ring, x through LDS with weights in registers, K split over the
+waves of a workgroup), ragged M/N/K, every split-K factor, F=14 (3 and 4 dots) and F=15; the
 one-launch digitize + GEMM path equals the oracle at 1-64 rows; the exactmm::linear op on
 load-time packed weights, with and without the shipped table (which picks the one-launch
 path at 16 rows for some shapes and not for others), equals the oracle.
@@ -81,12 +82,50 @@ def test_xw_two_byte_outputs_every_tile(tr):
     xp, wp = K.pack_digits(xd), K.pack_digits(wd)
     for bm, bn, r, nw in K.XW_SHAPES:
         cfg = (bm, bn, 64, nw, r, 8, 1)
-        yb = torch.full((M, N + 5), -1.0, device=DEV, dtype=torch.bfloat16)[:, :N]  # row stride 208
-        K.exact_linear_packed(xp, wp, Kd, F, tr, out=yb, cfg=cfg)
-        assert np.array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), want_b), ("bf16", cfg)
-        yh = torch.empty(M, N, device=DEV, dtype=torch.float16)
-        K.exact_linear_packed(xp, wp, Kd, F, tr, out=yh, cfg=cfg)
-        assert np.array_equal(yh.cpu().numpy().view(np.uint16), want_h), ("fp16", cfg)
+        full = torch.full((M, N + 5), -1.0, device=DEV, dtype=torch.bfloat16)  # row stride 208
+        K.exact_linear_packed(xp, wp, Kd, F, tr, out=full[:, :N], cfg=cfg)
+        got = full.cpu()
+        assert np.array_equal(got[:, :N].view(torch.int16).numpy().view(np.uint16), want_b), ("bf16", cfg)
+        assert torch.equal(got[:, N:], torch.full((M, 5), -1.0, dtype=torch.bfloat16)), ("bf16 padding", cfg)
+        fullh = torch.full((M, N + 3), -1.0, device=DEV, dtype=torch.float16)  # odd row stride: every piece element-wise
+        K.exact_linear_packed(xp, wp, Kd, F, tr, out=fullh[:, :N], cfg=cfg)
+        goth = fullh.cpu()
+        assert np.array_equal(goth[:, :N].numpy().view(np.uint16), want_h), ("fp16", cfg)
+        assert torch.equal(goth[:, N:], torch.full((M, 3), -1.0, dtype=torch.float16)), ("fp16 padding", cfg)
+
+
+XK_CFGS = tuple((bm, bn, 64 * kg, 8, 2, 8) for bm, bn, kg in K.XK_SHAPES)
+
+
+@pytest.mark.parametrize("F,tr", [(14, True), (14, False), (15, False)])
+@pytest.mark.parametrize("M,N,Kd", [(256, 384, 4096), (70, 203, 1000), (130, 1000, 512), (200, 96, 640)])
+def test_xk_kernel_bitwise(F, tr, M, N, Kd):
+    """The K-split kernel (K groups of waves reducing in LDS) for every instantiated tile, at 3
+    and 4 dots (shapes without a 4-dot instantiation, K splits that are not whole rounds and
+    K = 640, which has none, take the LDS-ring kernel) and split-K 1, 2, 4: fp32 output (lane
+    stores; int64 partials when split), bf16 into a strided view (staged tile; the padding
+    columns stay untouched), fp16 (staged, rows not 16-byte aligned) and F = 15 (offset terms),
+    every one equal to the oracle rounded once."""
+    x, w = stress_xw(M, N, Kd, seed=M + 3 * N)
+    xd, wd = K.digitize(x.to(DEV), F), K.digitize(w.to(DEV), F)
+    ref = oracle.exact_linear_c(np_digits(xd), np_digits(wd), F, tr)
+    ref_bits = f32_bits(ref)
+    want_b = oracle.bf16_rne_c(ref).reshape(M, N)
+    want_h = ref.astype(np.float16).view(np.uint16)
+    xp, wp = K.pack_digits(xd), K.pack_digits(wd)
+    for base, sk in itertools.product(XK_CFGS, (1, 2, 4)):
+        cfg = base + (sk,)
+        y = K.exact_linear_packed(xp, wp, Kd, F, tr, cfg=cfg)
+        assert np.array_equal(f32_bits(y.cpu().numpy()), ref_bits), ("fp32", cfg)
+        if sk == 1:
+            full = torch.full((M, N + 5), -1.0, device=DEV, dtype=torch.bfloat16)
+            K.exact_linear_packed(xp, wp, Kd, F, tr, out=full[:, :N], cfg=cfg)
+            got = full.cpu()
+            assert np.array_equal(got[:, :N].view(torch.int16).numpy().view(np.uint16), want_b), ("bf16", cfg)
+            assert torch.equal(got[:, N:], torch.full((M, 5), -1.0, dtype=torch.bfloat16)), ("bf16 padding", cfg)
+            yh = torch.empty(M, N, device=DEV, dtype=torch.float16)
+            K.exact_linear_packed(xp, wp, Kd, F, tr, out=yh, cfg=cfg)
+            assert np.array_equal(yh.cpu().numpy().view(np.uint16), want_h), ("fp16", cfg)
 
 
 FUSED_CFGS = tuple((16, 16 * nt, 128, nwk, c, 8, 1) for mt, nt, c, nwk in K.SMALL_SHAPES if mt == 1)

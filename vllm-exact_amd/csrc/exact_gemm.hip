@@ -79,6 +79,9 @@ int lds_stages(int bm, int bn, int want) {
 }
 
 // cfg tuple (BM, BN, BK, warps, stages, GM[, SK[, mma]]) -> kernel family and shape:
+//   BM >= 64, BK == 128 or 256, warps == 8, stages >= 2: on packed operands, the K-split kernel
+//     with tile BM x BN, KG = BK / 64 K groups of 8 / KG waves and R = stages weight register
+//     sets when instantiated (exact_xk_supported); otherwise the LDS-ring kernel below;
 //   BK == 64, warps 3, 4, 6 or 8: on packed operands, the x-through-LDS kernel with tile BM x BN,
 //     R = stages weight register sets and `warps` waves when instantiated (exact_xw_supported); otherwise, and
 //     on row-major digits, the LDS-ring kernel below with BM and BN clamped to 64..128;
@@ -96,7 +99,14 @@ int make_plan(int64_t K, const int32_t* cfg, int cfg_len, ExactPlan* out) {
   const int32_t SKr = cfg_len > 6 ? cfg[6] : 1;
   if (BM <= 0 || BN <= 0 || BK <= 0 || warps <= 0 || stages <= 0 || SKr <= 0) return VXA_ERR_ARG;
   ExactPlan p = {};
-  if (BK == 64 && (warps == 3 || warps == 4 || warps == 6 || warps == 8)) {
+  if (BM >= 64 && (BK == 128 || BK == 256) && warps == 8 && stages >= 2) {
+    p.family = kFamilyXk;
+    p.bm = BM;
+    p.bn = BN;
+    p.kg = BK / 64;
+    p.stages = stages;
+    p.nwk = warps;
+  } else if (BK == 64 && (warps == 3 || warps == 4 || warps == 6 || warps == 8)) {
     p.family = kFamilyXw;
     p.bm = BM;
     p.bn = BN;
@@ -161,9 +171,12 @@ int run_exact(const ExactPlan& pl, ExactParams& ep, int trunc, bool packed, bool
     err = hipGetLastError();
   } else if (pl.family == kFamilyXw && packed && exact_xw_supported(pl.bm, pl.bn, pl.stages, pl.nwk, trunc != 0)) {
     err = launch_exact_xw(pl, ep, trunc != 0, st);
-  } else if (pl.family == kFamilyXw || pl.family == kFamilyLds) {
+  } else if (pl.family == kFamilyXk && packed && exact_xk_supported(pl.bm, pl.bn, pl.kg, pl.stages, pl.nwk, trunc != 0) &&
+             exact_xk_whole_rounds(pl.kg, ep.kch, ep.kpad)) {
+    err = launch_exact_xk(pl, ep, trunc != 0, st);
+  } else if (pl.family == kFamilyXw || pl.family == kFamilyXk || pl.family == kFamilyLds) {
     ExactPlan lp = pl;
-    if (pl.family == kFamilyXw) {  // no x-through-LDS instantiation for it: nearest LDS-ring tile
+    if (pl.family != kFamilyLds) {  // no instantiation of its own family for it: nearest LDS-ring tile
       lp.bm = pl.bm >= 128 ? 128 : 64;
       lp.bn = pl.bn >= 128 ? 128 : 64;
       lp.stages = lds_stages(lp.bm, lp.bn, 4);

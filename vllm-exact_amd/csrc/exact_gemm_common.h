@@ -35,7 +35,7 @@ struct ExactParams {
 };
 
 // Kernel family and shape picked from a cfg tuple.
-enum ExactFamily { kFamilySmall = 0, kFamilyLds = 1, kFamilyScalar = 2, kFamilyXw = 3 };
+enum ExactFamily { kFamilySmall = 0, kFamilyLds = 1, kFamilyScalar = 2, kFamilyXw = 3, kFamilyXk = 4 };
 
 struct ExactPlan {
   int family;
@@ -45,6 +45,8 @@ struct ExactPlan {
   // LDS pipeline kernel: BM x BN workgroup tile, S ring stages; x-through-LDS kernel:
   // BM x BN workgroup tile, `stages` = R weight register sets, `nwk` = 3, 4, 6 or 8 waves
   int bm, bn, stages;
+  // K-split kernel: KG K groups of nwk / KG waves (bm, bn, stages as for the x-through-LDS kernel)
+  int kg;
   int64_t kch;
   int32_t sk;
 };
@@ -55,6 +57,22 @@ __device__ inline float exact_epilogue(int64_t tot, int32_t sxm, int32_t swn) {
   const int64_t e = -(int64_t)(sxm + swn);
   const double scale = __longlong_as_double((e + 1023) << 52);
   return (float)((double)tot * scale);
+}
+
+// The same value from the digit sums, tot = (hh 2^8 + md) 2^8 [+ ll]: every step below is exact
+// in fp64 (|tot| < 2^53, and scaling by a power of two in range is exact), so the conversion to
+// fp32 is the one rounding, as above.
+template <bool TRUNC>
+__device__ inline float exact_epilogue_digits(int32_t hh, int32_t md, int32_t ll, int32_t e) {
+  const double hm = __builtin_fma((double)hh, 256.0, (double)md);
+  if constexpr (TRUNC) return (float)__builtin_ldexp(hm, 8 - e);
+  return (float)__builtin_ldexp(__builtin_fma(hm, 256.0, (double)ll), -e);
+}
+
+// fp32 -> bf16 with round-to-nearest-even for finite values (the exact GEMM's outputs are finite).
+__device__ inline uint16_t f32_to_bf16_rne_finite(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
 // F == 15: 128*(cx + cw) + 128*128*K (kernels.py:96-97, 148-151)
@@ -90,3 +108,8 @@ hipError_t launch_exact_fused(const ExactPlan& pl, const void* x, int64_t ldx, c
 // Packed operands only (exact_gemm_xw.hip).
 hipError_t launch_exact_xw(const ExactPlan& pl, const ExactParams& ep, bool trunc, hipStream_t st);
 bool exact_xw_supported(int bm, int bn, int r, int waves, bool trunc);
+// K steps split over the waves of a workgroup (exact_gemm_xk.hip), packed operands only.
+hipError_t launch_exact_xk(const ExactPlan& pl, const ExactParams& ep, bool trunc, hipStream_t st);
+bool exact_xk_supported(int bm, int bn, int kg, int r, int waves, bool trunc);
+// The K-split kernel takes K splits that are whole rounds (2 * KG steps of 64).
+bool exact_xk_whole_rounds(int kg, int64_t kch, int64_t kpad);

@@ -1,0 +1,208 @@
+// Measured ceilings of the memory and matrix paths the exact GEMM and the paged decode
+// attention run on (MI355X, gfx950). These kernels compute nothing useful: each exercises one
+// path at a chosen depth of requests in flight, so a benchmark can report the achievable rate
+// beside the published peak.
+//
+//   stream   contiguous read of a large buffer, one chunk per workgroup (the weight stream)
+//   pages    read of 8 KiB pages in a given (permuted) order (the paged KV stream)
+//   l2       16-byte loads of an L2-resident buffer into VGPRs, or straight into LDS with
+//            global_load_lds_dwordx4, at Q loads in flight per lane
+//   lds      ds_read_b128 of LDS into VGPRs
+//   mfma     v_mfma_i32_16x16x64_i8 on 8 independent accumulators per wave
+//
+// Every kernel reads inside the buffer it is given (the host checks the sizes; the L2 probe
+// masks its offsets with a power of two that the buffer covers) and writes one int per thread
+// to `sink`, so no load can be optimised away. Thread 0 of each workgroup also writes the
+// shader-clock cycles its workgroup took, from which the host derives the clock rate.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+namespace {
+
+__device__ inline void finish(int* sink, int64_t* cycles, v4i acc, int64_t t0) {
+  // An impossible value keeps the loads live without a store per thread in the common case.
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5A5A5A5A) sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = 1;
+  if (threadIdx.x == 0) cycles[blockIdx.x] = (int64_t)clock64() - t0;
+}
+
+// Workgroup b reads bytes [b * per_wg, (b + 1) * per_wg): Q 16-byte non-temporal loads per lane
+// in flight. per_wg is a multiple of 16 * blockDim.x * Q (host-checked).
+template <int Q>
+__global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf, int64_t per_wg16, int* sink,
+                                                     int64_t* cycles) {
+  const int64_t t0 = clock64();
+  const v4i* p = buf + (int64_t)blockIdx.x * per_wg16;
+  const int64_t T = blockDim.x;
+  v4i acc = {0, 0, 0, 0};
+  for (int64_t i = threadIdx.x; i < per_wg16; i += T * Q) {
+    v4i a[Q];
+#pragma unroll
+    for (int u = 0; u < Q; ++u) a[u] = __builtin_nontemporal_load(p + i + u * T);
+#pragma unroll
+    for (int u = 0; u < Q; ++u) acc ^= a[u];
+  }
+  finish(sink, cycles, acc, t0);
+}
+
+// Workgroup b reads pages pages[b * ppw .. (b + 1) * ppw) of 8 KiB each; the 512 lanes of a
+// workgroup cover one page per round (one 16-byte load each), Q pages in flight.
+template <int Q>
+__global__ __launch_bounds__(512) void pages_kernel(const v4i* __restrict__ buf, const int32_t* __restrict__ pages,
+                                                    int ppw, int* sink, int64_t* cycles) {
+  const int64_t t0 = clock64();
+  const int32_t* mine = pages + (int64_t)blockIdx.x * ppw;
+  v4i acc = {0, 0, 0, 0};
+  for (int i = 0; i < ppw; i += Q) {
+    v4i a[Q];
+#pragma unroll
+    for (int u = 0; u < Q; ++u) a[u] = __builtin_nontemporal_load(buf + (int64_t)mine[i + u] * 512 + threadIdx.x);
+#pragma unroll
+    for (int u = 0; u < Q; ++u) acc ^= a[u];
+  }
+  finish(sink, cycles, acc, t0);
+}
+
+// L2-resident loads: each wave walks a 16 KiB window of the buffer per round (offsets masked
+// into [0, n16)), Q 1-KiB wave loads in flight. LDS = 1: global_load_lds_dwordx4 into a ring of
+// Q 1-KiB slots per wave (never read: only the arrival is waited for).
+template <int Q, bool LDS>
+__global__ __launch_bounds__(1024) void l2_kernel(const v4i* __restrict__ buf, int64_t mask16, int rounds, int* sink,
+                                                  int64_t* cycles) {
+  __shared__ __attribute__((aligned(1024))) int8_t ring[LDS ? 16 * Q * 1024 : 16];
+  const int64_t t0 = clock64();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t base = ((int64_t)blockIdx.x * 16 + wave) * 1024;  // in 16-byte units
+  v4i acc = {0, 0, 0, 0};
+  for (int r = 0; r < rounds; ++r) {
+    if constexpr (LDS) {
+#pragma unroll
+      for (int u = 0; u < Q; ++u) {
+        const v4i* src = buf + ((base + (int64_t)(r * Q + u) * 64 + lane) & mask16);
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(ring + (wave * Q + u) * 1024), 16, 0, 0);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring is refilled next round
+    } else {
+      v4i a[Q];
+#pragma unroll
+      for (int u = 0; u < Q; ++u) a[u] = buf[(base + (int64_t)(r * Q + u) * 64 + lane) & mask16];
+#pragma unroll
+      for (int u = 0; u < Q; ++u) acc ^= a[u];
+    }
+  }
+  if constexpr (LDS) {
+    __syncthreads();
+    acc = *reinterpret_cast<const v4i*>(ring + (threadIdx.x % (16 * Q * 64)) * 16);
+  }
+  finish(sink, cycles, acc, t0);
+}
+
+// ds_read_b128: each lane reads 16 bytes per instruction from a 64 KiB LDS tile, 8 reads in
+// flight.
+__global__ __launch_bounds__(1024) void lds_kernel(int rounds, int* sink, int64_t* cycles) {
+  __shared__ __attribute__((aligned(1024))) int8_t tile[64 * 1024];
+  for (int i = threadIdx.x; i < 4096; i += blockDim.x) reinterpret_cast<v4i*>(tile)[i] = v4i{i, i + 1, i + 2, i + 3};
+  __syncthreads();
+  const int64_t t0 = clock64();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v4i acc = {0, 0, 0, 0};
+  for (int r = 0; r < rounds; ++r) {
+    v4i a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      a[u] = *reinterpret_cast<const v4i*>(tile + (((wave * 8 + u + r) & 63) * 1024) + lane * 16);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= a[u];
+  }
+  finish(sink, cycles, acc, t0);
+}
+
+// v_mfma_i32_16x16x64_i8 on 8 independent accumulators per wave.
+__global__ __launch_bounds__(1024) void mfma_kernel(int rounds, int* sink, int64_t* cycles) {
+  const int64_t t0 = clock64();
+  const v4i a = {(int)threadIdx.x, 3, 5, 7}, b = {11, 13, (int)blockIdx.x, 17};
+  v4i c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = v4i{i, 0, 0, 0};
+  for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c[i], 0, 0, 0);
+  }
+  v4i acc = c[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) acc ^= c[i];
+  finish(sink, cycles, acc, t0);
+}
+
+}  // namespace
+
+extern "C" {
+
+// Status: 0 ok, 1 bad argument, 4 launch error.
+int vxf_stream(const void* buf, int64_t buf_bytes, int64_t per_wg_bytes, int blocks, int threads, int q, int* sink,
+               int64_t* cycles, void* stream) {
+  if (!buf || !sink || !cycles || blocks <= 0 || (threads != 256 && threads != 512)) return 1;
+  if (q != 4 && q != 8) return 1;
+  if (per_wg_bytes <= 0 || per_wg_bytes % (16LL * threads * q) != 0) return 1;
+  if ((int64_t)blocks * per_wg_bytes > buf_bytes) return 1;
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t n16 = per_wg_bytes / 16;
+  const auto* p = (const v4i*)buf;
+  if (q == 4) hipLaunchKernelGGL(stream_kernel<4>, dim3(blocks), dim3(threads), 0, st, p, n16, sink, cycles);
+  else if (q == 8) hipLaunchKernelGGL(stream_kernel<8>, dim3(blocks), dim3(threads), 0, st, p, n16, sink, cycles);
+  else return 1;
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// pages: int32 [blocks * ppw] page indices, each in [0, buf_bytes / 8192) (the caller checks).
+int vxf_pages(const void* buf, int64_t buf_bytes, const int32_t* pages, int blocks, int ppw, int q, int* sink,
+              int64_t* cycles, void* stream) {
+  if (q != 1 && q != 2 && q != 4) return 1;
+  if (!buf || !pages || !sink || !cycles || blocks <= 0 || ppw <= 0 || ppw % q != 0 || buf_bytes < 8192) return 1;
+  const hipStream_t st = (hipStream_t)stream;
+  const auto* p = (const v4i*)buf;
+  if (q == 1) hipLaunchKernelGGL(pages_kernel<1>, dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles);
+  else if (q == 2) hipLaunchKernelGGL(pages_kernel<2>, dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles);
+  else if (q == 4) hipLaunchKernelGGL(pages_kernel<4>, dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles);
+  else return 1;
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// l2: buf_bytes a power of two >= 16 KiB; lds = 0 (VGPR loads) or 1 (direct-to-LDS).
+int vxf_l2(const void* buf, int64_t buf_bytes, int lds, int q, int waves, int blocks, int rounds, int* sink,
+           int64_t* cycles, void* stream) {
+  if (!buf || !sink || !cycles || blocks <= 0 || rounds <= 0) return 1;
+  if (buf_bytes < 16384 || (buf_bytes & (buf_bytes - 1)) != 0) return 1;
+  if (waves != 4 && waves != 8 && waves != 16) return 1;
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t mask = buf_bytes / 16 - 1;
+  const auto* p = (const v4i*)buf;
+  const dim3 g(blocks), b(64 * waves);
+#define VXF_L2(Q_)                                                                   \
+  if (q == Q_) {                                                                     \
+    if (lds) hipLaunchKernelGGL((l2_kernel<Q_, true>), g, b, 0, st, p, mask, rounds, sink, cycles); \
+    else hipLaunchKernelGGL((l2_kernel<Q_, false>), g, b, 0, st, p, mask, rounds, sink, cycles);    \
+    return hipGetLastError() == hipSuccess ? 0 : 4;                                  \
+  }
+  VXF_L2(1) VXF_L2(2) VXF_L2(4) VXF_L2(8)
+#undef VXF_L2
+  return 1;
+}
+
+int vxf_lds(int waves, int blocks, int rounds, int* sink, int64_t* cycles, void* stream) {
+  if (!sink || !cycles || blocks <= 0 || rounds <= 0 || (waves != 4 && waves != 8 && waves != 16)) return 1;
+  hipLaunchKernelGGL(lds_kernel, dim3(blocks), dim3(64 * waves), 0, (hipStream_t)stream, rounds, sink, cycles);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+int vxf_mfma(int waves, int blocks, int rounds, int* sink, int64_t* cycles, void* stream) {
+  if (!sink || !cycles || blocks <= 0 || rounds <= 0 || (waves != 4 && waves != 8 && waves != 16)) return 1;
+  hipLaunchKernelGGL(mfma_kernel, dim3(blocks), dim3(64 * waves), 0, (hipStream_t)stream, rounds, sink, cycles);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+}  // extern "C"

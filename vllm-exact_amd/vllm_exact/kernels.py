@@ -255,7 +255,10 @@ def exact_linear_bf16x(x, wp, K, F, trunc=False, out=None, cfg=None):
 # * LDS-ring kernel (BM, BN >= 64, 4 waves, stages >= 2): BM x BN tile, `stages`-deep ring
 #   of direct-to-LDS loads;
 # * x-through-LDS kernel (BK = 64, packed digits): BM x BN tile, `warps` = 4 or 8 waves,
-#   `stages` = weight register sets in flight per wave.
+#   `stages` = weight register sets in flight per wave;
+# * K-split kernel (BM >= 64, BK = 64 * KG with KG = 2 or 4 K groups, 8 waves, stages = 2,
+#   packed digits): BM x BN tile, the waves of a K group covering all BM rows of BN / (8 / KG)
+#   columns each over every KG-th pair of K steps.
 # BK otherwise only rounds split-K chunks; GM is accepted for the reference's format.
 SMALL_SHAPES = [(1, 1, 1, 4), (1, 1, 1, 8), (1, 1, 1, 16), (1, 1, 2, 4), (1, 1, 2, 8), (1, 1, 2, 16), (1, 1, 4, 4),
                 (1, 1, 4, 8), (1, 1, 4, 16), (1, 2, 1, 4), (1, 2, 1, 8), (1, 2, 1, 16), (1, 2, 2, 4), (1, 2, 2, 8),
@@ -270,9 +273,12 @@ XW_SHAPES = [(32, 128, 4, 4), (32, 256, 4, 4), (64, 64, 4, 4), (64, 128, 4, 4), 
              (128, 192, 4, 4), (64, 128, 4, 8), (64, 192, 4, 8), (64, 256, 4, 8), (128, 128, 4, 8),
              (128, 192, 3, 8), (128, 192, 4, 8), (128, 256, 2, 8), (64, 96, 4, 6), (64, 96, 6, 6), (64, 96, 8, 6),
              (64, 96, 4, 3), (64, 96, 6, 3)]  # (BM, BN, weight sets, waves); BK = 64
+XK_SHAPES = [(128, 192, 2), (128, 128, 2), (64, 96, 4), (64, 64, 4), (64, 128, 2), (64, 192, 2)]  # (BM, BN, KG)
+XK_FOUR_DOTS = [(64, 96, 4), (64, 64, 4), (64, 128, 2), (64, 192, 2)]  # the shapes with 4-dot instantiations
 EXACT_CFGS = ([(16 * mt, 16 * nt, 128, nwk, c, 8) for mt, nt, c, nwk in SMALL_SHAPES]
               + [(bm, bn, 128, 4, st, 8) for bm, bn, st in LDS_SHAPES]
-              + [(bm, bn, 64, nw, r, 8) for bm, bn, r, nw in XW_SHAPES])
+              + [(bm, bn, 64, nw, r, 8) for bm, bn, r, nw in XW_SHAPES]
+              + [(bm, bn, 64 * kg, 8, 2, 8) for bm, bn, kg in XK_SHAPES])
 AUTOTUNE_SPLITS = (1, 2, 4)
 _CFG_CACHE = {}
 
