@@ -25,6 +25,7 @@ Also reported, from the same run:
 * `decode_step`: the synthetic decode step of the ~9B hybrid (32 layers of the four exact
   linears, paged attention on 8 of them, exact lm_head 4096->151936) at batch/context 256/1K,
   64/8K and 16/16K: ms per step as a HIP graph, the same step with hipBLASLt bf16 linears,
+  for each leg the time of its linears, attention calls and glue each in a graph of its own,
   bitwise batch invariance of the logits, and a CPU estimate from the oracle's timings;
 * bit-exactness of the benchmarked outputs against the CPU oracle (sampled rows);
 * `per_op_f15`: the 4-dot variant, the same sweep at F = 15 (offset digits) with the table
@@ -58,7 +59,7 @@ MS = [1, 16, 64, 256]
 F, TRUNC, NDOTS = 14, True, 3
 ATTN_CASES = [(64, 8192), (16, 16384), (256, 1024)]
 DECODE_CASES = [(256, 1024), (64, 8192), (16, 16384)]  # (batch, context) of the decode-step emulation
-HIDDEN, VOCAB, LAYERS, ATTN_EVERY = 4096, 151936, 32, 4
+HIDDEN, VOCAB, LAYERS, ATTN_EVERY, FFN = 4096, 151936, 32, 4, 12288
 ATT_H, ATT_KV, ATT_D, ATT_BS = 32, 8, 128, 16
 
 
@@ -126,6 +127,71 @@ class DecodeStep:
             half = gu.shape[1] // 2
             h = h + lin(torch.nn.functional.silu(gu[:, :half]) * gu[:, half:], ws["down"])
         return lin(rownorm(h), self.lm)
+
+    def parts(self, B, caches, bt, sl, gen):
+        """The three parts of one step, each issued on its own over inputs of the step's shapes,
+        for a time breakdown: every linear of the step (the 4 x layers layer linears and the
+        lm_head), every attention call, and the glue between them (row rescales, residual adds,
+        the gated SiLU). Each callable takes `exact` (False: the hipBLASLt bf16 linears)."""
+        torch, dev = self.torch, self.dev
+        r = lambda *shape: torch.randn(*shape, device=dev, generator=gen).to(torch.bfloat16)
+        xh, xf = r(B, HIDDEN), r(B, FFN)
+        gu, q = r(B, 2 * FFN), r(B, ATT_H, ATT_D)
+        o = torch.empty(B, ATT_H, ATT_D, device=dev, dtype=torch.bfloat16)
+
+        def linears(exact):
+            for ws in self.layers:
+                for name, x in (("qkv", xh), ("o", xh), ("gate_up", xh), ("down", xf)):
+                    torch.ops.exactmm.linear(x, *ws[name][0]) if exact else torch.matmul(x, ws[name][1].T)
+            torch.ops.exactmm.linear(xh, *self.lm[0]) if exact else torch.matmul(xh, self.lm[1].T)
+
+        def attention(exact):
+            for _, kc, vc in caches:
+                self.P.paged_decode(q, kc, vc, bt, sl, ATT_D ** -0.5, o, B, self.P.MAX_LEN)
+
+        def rownorm(t):
+            e = torch.frexp(t.abs().amax(dim=-1, keepdim=True).float()).exponent
+            return torch.ldexp(t.float(), -e).to(torch.bfloat16)
+
+        def glue(exact):
+            h = xh
+            for _ in self.layers:
+                rownorm(h)  # before the QKV linear
+                h = h + xh  # residual add of the o output
+                rownorm(h)  # before gate_up
+                torch.nn.functional.silu(gu[:, :FFN]) * gu[:, FFN:]  # the down linear's input
+                h = h + xh  # residual add of the down output
+            rownorm(h)  # before the lm_head
+
+        return {"linears": linears, "attention": attention, "glue": glue}
+
+
+def graph_ms(torch, fn, replays=10):
+    """Median milliseconds of one replay of a HIP graph holding fn() (captured after a warm
+    call on a side stream)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    del g
+    torch.cuda.synchronize()
+    return sorted(ts)[len(ts) // 2]
 
 
 def gemm_bytes(M, N, K):
@@ -278,16 +344,15 @@ def cpu_baseline_leg(torch, K, np, oracle, step_bytes, ops, budget_s):
         x = torch.randn(M, Kd, generator=g).to(torch.bfloat16).float()
         t_dig, _ = timed(lambda: K.digitize_torch(x, F), 0.05)
         xd = K.digitize_torch(x, F)
-        # calibrate on 64 weight rows, then one timed sample sized to the op's share of the budget
+        # calibrate on 64 weight rows, then a sample sized so that about three repetitions fill
+        # the op's share of the budget; the time is the mean over the repetitions timed
         wd = K.digitize_torch(wfull[name][:64], F)
         t0 = time.perf_counter()
         K.exact_linear_torch(xd, wd, F, TRUNC)
         per_row = (time.perf_counter() - t0) / 64
-        ns = int(min(N, 2048, max(64, per_op_s / max(per_row, 1e-9)))) // 16 * 16
+        ns = int(min(N, 2048, max(64, per_op_s / 3 / max(per_row, 1e-9)))) // 16 * 16
         wd = K.digitize_torch(wfull[name][:ns], F)
-        t0 = time.perf_counter()
-        K.exact_linear_torch(xd, wd, F, TRUNC)
-        t_lin, reps = time.perf_counter() - t0, 1
+        t_lin, reps = timed(lambda: K.exact_linear_torch(xd, wd, F, TRUNC), per_op_s * 2 / 3)
         t = t_dig + t_lin * N / ns
         op_s[(M, name)] = t
         total_s += t
@@ -296,7 +361,8 @@ def cpu_baseline_leg(torch, K, np, oracle, step_bytes, ops, budget_s):
                os_cpu_count=ncpu, torch_threads=threads,
                sample="torch int64 statements of the reference's CPU path (kernels.digitize_torch + "
                       "kernels.exact_linear_torch) on every host thread; each sweep op on its first weight rows, "
-                      "time extrapolated linearly in N (labelled extrapolated); config 1 in full: "
+                      "mean over the repetitions shown (xN), time extrapolated linearly in N (labelled "
+                      "extrapolated); config 1 in full: "
                       + "; ".join(desc),
                step_ms_extrapolated=round(total_s * 1e3, 1), config1_full=c1)
 
@@ -564,7 +630,12 @@ def floors(args):
                    "cycles_per_mfma_per_simd": round(cy / per_simd, 2), "TOPS": round(ops / us / 1e6, 1)})
         log("mfma", mf[-1])
     out["mfma_i8_16x16x64"] = mf
-    ghz = statistics.median(r["ghz"] for r in mf)
+    # with one wave per SIMD the first wave's cycles span the whole workgroup; with more, a
+    # wave can finish before the others, so its cycle count says nothing about the clock
+    ghz = mf[0]["ghz"]
+    for r in mf[1:]:
+        r.pop("ghz")
+        r.pop("cycles_per_mfma_per_simd")
 
     # LDS reads: ds_read_b128, 8 in flight per lane
     ld = []
@@ -572,7 +643,7 @@ def floors(args):
         rounds = 2048
         us, cy = timed(lambda: check(lib.vxf_lds(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())), ncu)
         b = rounds * 8 * 64 * 16 * waves
-        ld.append({"waves_per_cu": waves, "us": round(us, 1), "bytes_per_clk_per_cu": round(b / cy, 1)})
+        ld.append({"waves_per_cu": waves, "us": round(us, 1), "bytes_per_clk_per_cu": round(b / (us * 1e3 * ghz), 1)})
         log("lds", ld[-1])
     out["lds_read_b128"] = ld
 
@@ -587,7 +658,7 @@ def floors(args):
                                                         sink.data_ptr(), cyc.data_ptr(), st())), ncu)
                 b = rounds * q * 1024 * waves
                 l2.append({"path": "lds" if lds else "vgpr", "waves_per_cu": waves, "loads_in_flight": q,
-                           "us": round(us, 1), "bytes_per_clk_per_cu": round(b / cy, 1),
+                           "us": round(us, 1), "bytes_per_clk_per_cu": round(b / (us * 1e3 * ghz), 1),
                            "TBps": round(b * ncu / us / 1e6, 2)})
                 log("l2", l2[-1])
     out["l2_load_16B"] = l2
@@ -603,7 +674,7 @@ def floors(args):
         for blocks in (256, 512, 1024):
             for q in (4, 8):
                 per_wg = nbytes // blocks
-                per_wg -= per_wg % (16 * 512 * q)
+                per_wg -= per_wg % (16 * 512)
                 if per_wg <= 0:
                     continue
 
@@ -613,7 +684,7 @@ def floors(args):
 
                 us = time_graph(call, rotations=rot)
                 row = {"blocks": blocks, "loads_in_flight": q, "us": round(us, 2),
-                       "bytes_read": per_wg * blocks, "hbm_frac": round(per_wg * blocks / us / 1e6 / HBM_PEAK_GBS, 3)}
+                       "bytes_read": per_wg * blocks, "hbm_frac": round(per_wg * blocks / us / 1e3 / HBM_PEAK_GBS, 3)}
                 if best is None or row["us"] < best["us"]:
                     best = row
         stream_rows.append({"weights_of": name, "bytes": nbytes, "copies": rot, **best})
@@ -645,7 +716,7 @@ def floors(args):
     us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, seq.data_ptr(), 2048, npg // 2048, 2,
                                               sink.data_ptr(), cyc.data_ptr(), st())), 2048)
     out["sequential_8k_pages_TBps"] = round(nb / us / 1e6, 2)
-    out["ghz_under_mfma"] = ghz
+    out["ghz_one_wave_per_simd_mfma"] = ghz
     print(json.dumps(out), flush=True)
 
 
@@ -890,33 +961,25 @@ def main():
             caches, bt, sl = model.kv(B, L, gen)
             h0 = torch.randn(B, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
             rec = dict(B=B, L=L)
-            full = None
+            out = {}
+
+            def whole(exact):
+                out["logits"] = model.step(h0, caches, bt, sl, exact)
+
+            parts = model.parts(B, caches, bt, sl, gen)
             for exact in (True, False):
-                side = torch.cuda.Stream()
-                side.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(side):
-                    model.step(h0, caches, bt, sl, exact)
-                torch.cuda.current_stream().wait_stream(side)
-                torch.cuda.synchronize()
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    logits = model.step(h0, caches, bt, sl, exact)
-                for _ in range(2):
-                    g.replay()
-                torch.cuda.synchronize()
-                ts = []
-                for _ in range(10):
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    g.replay()
-                    e1.record()
-                    e1.synchronize()
-                    ts.append(e0.elapsed_time(e1))
-                rec["exact_ms" if exact else "bf16_hipblaslt_ms"] = round(float(np.median(ts)), 3)
+                leg = "exact" if exact else "bf16_hipblaslt"
+                rec[leg + "_ms"] = round(graph_ms(torch, lambda: whole(exact)), 3)
                 if exact:
-                    full = logits.clone()
-                del g, logits
-                torch.cuda.synchronize()
+                    full = out["logits"].clone()
+                out.clear()
+                # each part of the step timed on its own (graph replay); the remainder is what
+                # the parts do not account for when run back to back in one graph
+                br = {name: round(graph_ms(torch, lambda: fn(exact)), 3) for name, fn in parts.items()}
+                br["sum_of_parts"] = round(sum(br.values()), 3)
+                br["whole_minus_parts"] = round(rec[leg + "_ms"] - br["sum_of_parts"], 3)
+                rec[leg + "_breakdown_ms"] = br
+            del parts
             # bitwise batch invariance of the exact logits: first and last request alone, and
             # the two of them as a batch in reversed order
             ok = True

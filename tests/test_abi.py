@@ -167,3 +167,28 @@ def test_noalloc_entry_refuses_problems_beyond_its_scratch():
     # bad arguments are still refused first
     assert L.vxa_exact_linear_op_noalloc(fake, nx.VXA_BF16, 64, fake, fake, fake, fake, nx.VXA_BF16, 64, 1, 64,
                                          64, 16, 1, cfg, 7, None) == nx.VXA_ERR_ARG
+
+
+def test_noalloc_entry_checks_every_argument_before_launching():
+    """A call the GEMM stage would refuse is refused before the digitize stage writes the shared
+    scratch: the pointers below are never dereferenced (no GPU is needed), so a launch would
+    show up as a crash or a launch error, not as VXA_ERR_ARG."""
+    L = nx.lib()
+    fake = 0x1000
+    cfg = (ctypes.c_int32 * 7)(16, 64, 128, 4, 1, 8, 1)
+
+    def call(x=fake, xd=nx.VXA_BF16, ldx=64, wp=fake, cw=fake, sw=fake, out=fake, od=nx.VXA_BF16, ldo=64, m=2, n=64,
+             k=64, f=14, trunc=1):
+        return L.vxa_exact_linear_op_noalloc(x, xd, ldx, wp, cw, sw, out, od, ldo, m, n, k, f, trunc, cfg, 7, None)
+
+    assert call(od=9) == nx.VXA_ERR_ARG
+    assert call(ldo=10) == nx.VXA_ERR_ARG
+    assert call(out=None) == nx.VXA_ERR_ARG
+    assert call(wp=None) == nx.VXA_ERR_ARG
+    assert call(wp=fake + 8) == nx.VXA_ERR_ARG  # packed weights are read 16 bytes at a time
+    assert call(sw=None) == nx.VXA_ERR_ARG
+    assert call(f=15, trunc=0, cw=None) == nx.VXA_ERR_ARG
+    assert call(xd=7) == nx.VXA_ERR_ARG
+    assert call(ldx=10) == nx.VXA_ERR_ARG
+    assert call(x=None) == nx.VXA_ERR_ARG
+    assert call(m=0) == nx.VXA_OK

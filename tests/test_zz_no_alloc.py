@@ -65,3 +65,49 @@ def test_noalloc_op_fp32_output_and_fp32_input():
     want = K.exact_linear_packed(K.digitize_packed(x, plugin.F), wp, Kd, plugin.F, plugin.TRUNC, cfg=cfg)
     got = noalloc(x, wp, Kd, plugin.F, plugin.TRUNC, torch.empty(M, N, device=DEV), cfg)
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_noalloc_op_under_graph_capture():
+    """The entry point captured in a HIP graph: one warm call outside capture, then the call
+    captured; each replay (after new activations are copied in, with eager work and a
+    synchronisation between replays) equals exact_linear_packed on the same input, and the
+    captured call allocates nothing (torch's allocated bytes grow by no more than an empty
+    capture makes them grow)."""
+    g = torch.Generator().manual_seed(11)
+    M, N, Kd, F, trunc, cfg = 24, 768, 4096, 14, True, (16, 64, 128, 4, 1, 8, 2)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wp = K.digitize_packed(w, F)
+    x = torch.empty(M, Kd, device=DEV, dtype=torch.bfloat16)
+    out = torch.empty(M, N, device=DEV, dtype=torch.bfloat16)
+    x.copy_(torch.randn(M, Kd, generator=g).to(torch.bfloat16))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        noalloc(x, wp, Kd, F, trunc, out, cfg)  # warm call: looks up the scratch address
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    # Capturing a graph costs torch a few bytes of its own (the RNG state it keeps per graph):
+    # measured on an empty capture, after a first capture has paid any one-time cost.
+    empties = [torch.cuda.CUDAGraph() for _ in range(2)]
+    with torch.cuda.graph(empties[0]):
+        pass
+    before = torch.cuda.memory_allocated()
+    with torch.cuda.graph(empties[1]):
+        pass
+    capture_cost = torch.cuda.memory_allocated() - before
+    graph = torch.cuda.CUDAGraph()
+    before = torch.cuda.memory_allocated()
+    with torch.cuda.graph(graph):
+        noalloc(x, wp, Kd, F, trunc, out, cfg)
+    assert torch.cuda.memory_allocated() - before == capture_cost
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        x.copy_((torch.randn(M, Kd, generator=g) * (rep + 1)).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = K.exact_linear_packed(K.digitize_packed(x, F), wp, Kd, F, trunc,
+                                     out=torch.empty(M, N, device=DEV, dtype=torch.bfloat16), cfg=cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
+    del graph, empties

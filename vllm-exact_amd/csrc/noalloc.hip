@@ -7,7 +7,8 @@
 // VXA_NOALLOC_SCRATCH_BYTES. Each GPU holds its own copy of the array until the process ends;
 // its device address is looked up once per device (hipGetSymbolAddress) at the first call on
 // that device and kept. Calls that overlap on one GPU share the array and race: a caller
-// serialises them (one stream, or events). Every byte the kernels read from the array is
+// serialises them (one stream, or events). Arguments are checked on the host before anything is
+// launched, so a refused call leaves the array alone. Every byte the kernels read from the array is
 // written earlier in the same call (the digitize kernel writes every packed byte, padding
 // included; each split writes its whole partial tile), so nothing needs clearing between
 // calls.
@@ -56,6 +57,13 @@ extern "C" int vxa_exact_linear_op_noalloc(const void* x, int x_dtype, int64_t l
   if (rc != VXA_OK) return rc;
   if (m == 0 || n == 0) return VXA_OK;
   if (k == 0) return VXA_ERR_UNSUPPORTED;  // K = 0 has no packed form
+  // Every argument both launches check, checked here first: a call refused with VXA_ERR_ARG
+  // launches nothing, so it cannot overwrite the scratch of a call still running on this GPU.
+  if (!x || ldx < k || (x_dtype != VXA_F32 && x_dtype != VXA_BF16 && x_dtype != VXA_F16)) return VXA_ERR_ARG;
+  if (!wp || !sw || !out || ldo < n || (out_dtype != VXA_F32 && out_dtype != VXA_BF16 && out_dtype != VXA_F16))
+    return VXA_ERR_ARG;
+  if ((uintptr_t)wp % 16 || (f == 15 && !cw)) return VXA_ERR_ARG;
+  if (cdiv<int64_t>(m, 16) * 16 > 0x7FFFFFFFLL) return VXA_ERR_UNSUPPORTED;
   const size_t xp_bytes = align256(vxa_packed_bytes(m, k));
   const size_t sum_bytes = align256((size_t)m * sizeof(int32_t));
   if (xp_bytes > kScratchBytes || ws_bytes > kScratchBytes || xp_bytes + 2 * sum_bytes + ws_bytes > kScratchBytes)

@@ -30,7 +30,8 @@ __device__ inline void finish(int* sink, int64_t* cycles, v4i acc, int64_t t0) {
 }
 
 // Workgroup b reads bytes [b * per_wg, (b + 1) * per_wg): Q 16-byte non-temporal loads per lane
-// in flight. per_wg is a multiple of 16 * blockDim.x * Q (host-checked).
+// in flight, then the remainder one load per lane at a time. per_wg is a multiple of
+// 16 * blockDim.x (host-checked).
 template <int Q>
 __global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf, int64_t per_wg16, int* sink,
                                                      int64_t* cycles) {
@@ -38,13 +39,15 @@ __global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf
   const v4i* p = buf + (int64_t)blockIdx.x * per_wg16;
   const int64_t T = blockDim.x;
   v4i acc = {0, 0, 0, 0};
-  for (int64_t i = threadIdx.x; i < per_wg16; i += T * Q) {
+  int64_t i = threadIdx.x;
+  for (; i + (Q - 1) * T < per_wg16; i += T * Q) {
     v4i a[Q];
 #pragma unroll
     for (int u = 0; u < Q; ++u) a[u] = __builtin_nontemporal_load(p + i + u * T);
 #pragma unroll
     for (int u = 0; u < Q; ++u) acc ^= a[u];
   }
+  for (; i < per_wg16; i += T) acc ^= __builtin_nontemporal_load(p + i);
   finish(sink, cycles, acc, t0);
 }
 
@@ -147,7 +150,7 @@ int vxf_stream(const void* buf, int64_t buf_bytes, int64_t per_wg_bytes, int blo
                int64_t* cycles, void* stream) {
   if (!buf || !sink || !cycles || blocks <= 0 || (threads != 256 && threads != 512)) return 1;
   if (q != 4 && q != 8) return 1;
-  if (per_wg_bytes <= 0 || per_wg_bytes % (16LL * threads * q) != 0) return 1;
+  if (per_wg_bytes <= 0 || per_wg_bytes % (16LL * threads) != 0) return 1;
   if ((int64_t)blocks * per_wg_bytes > buf_bytes) return 1;
   const hipStream_t st = (hipStream_t)stream;
   const int64_t n16 = per_wg_bytes / 16;

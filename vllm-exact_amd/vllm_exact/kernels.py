@@ -338,11 +338,17 @@ def _next_pow2(v):
 
 
 def autotune_exact(xd, wd, F, trunc):
-    """Time every candidate (and split-K factor) with HIP events and cache the fastest
-    (kernels.py:292-316). Candidates the kernels reject are skipped."""
+    """Time every candidate (and split-K factor) and cache the fastest (kernels.py:292-316).
+    Each candidate is timed by HIP-graph replay on the weights as given, the method of the
+    reference's tuner (scripts/tune_table.py:38-57): a loop of launches timed with events
+    favours configs with fewer launches and never picks split-K, where a graph, as vLLM's
+    decode runs the op, does not. Candidates the kernels reject are skipped."""
+    from .graph_timing import time_graph
+
     M, K = xd[0].shape
     N = wd[0].shape[0]
     key = (M, N, K, F, bool(trunc))
+    out = torch.empty((M, N), device=xd[0].device, dtype=torch.float32)
     best = None
     for c in EXACT_CFGS:
         if c[0] > max(16, _next_pow2(M)):
@@ -350,16 +356,10 @@ def autotune_exact(xd, wd, F, trunc):
         for sk in AUTOTUNE_SPLITS:
             cand = tuple(c) + (sk,)
             try:
-                fn = lambda: exact_linear(xd, wd, F, trunc, cfg=cand)
-                fn()
+                exact_linear(xd, wd, F, trunc, out=out, cfg=cand)
                 torch.cuda.synchronize()
-                st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                st.record()
-                for _ in range(10):
-                    fn()
-                en.record()
-                torch.cuda.synchronize()
-                t = st.elapsed_time(en)
+                t = time_graph(lambda i, cand=cand: exact_linear(xd, wd, F, trunc, out=out, cfg=cand),
+                               calls_per_replay=10, replays=5)
             except (NotImplementedError, ValueError, RuntimeError):
                 continue
             if best is None or t < best[0]:
