@@ -419,6 +419,7 @@ def parse():
 
 
 TRAFFIC_SUMMARY = ROOT / "profiles" / "exact_gemm_m256_gate_up_hbm_traffic.md"
+COUNTERS_SUMMARY = ROOT / "profiles" / "exact_gemm_and_attention_counters.md"
 
 
 def kernel_sources_sha16():
@@ -458,6 +459,30 @@ def read_traffic(kernel_cfg):
             f"this library's sources (sha16 {vals['kernel_sources_sha16']}), calibrated on a 1 GiB copy")
     except (KeyError, ValueError):
         return None, f"{TRAFFIC_SUMMARY.name} is incomplete"
+
+
+def read_op_traffic():
+    """Per sweep op, the HBM bytes per launch (GEMM + split-K finalize) measured by the
+    FETCH_SIZE and WRITE_SIZE passes of `bench.py --profile-counters`, as recorded in
+    COUNTERS_SUMMARY: its `kernel_sources_sha16` line and one `traffic M:<M> op:<op> cfg:<cfg>
+    = <bytes>` line per op. Returns ({(M, op): (bytes, cfg)}, note); empty when the record was
+    made on a library built from other sources."""
+    if not COUNTERS_SUMMARY.exists():
+        return {}, "no counters summary"
+    out, sha = {}, None
+    for line in COUNTERS_SUMMARY.read_text().splitlines():
+        if not line.startswith("    ") or "=" not in line:
+            continue
+        k, v = line.strip().rsplit("=", 1)
+        k, v = k.strip(), v.strip()
+        if k == "kernel_sources_sha16":
+            sha = v
+        elif k.startswith("traffic "):
+            f = dict(t.split(":", 1) for t in k.split()[1:])
+            out[(int(f["M"]), f["op"])] = (int(v), json.loads(f["cfg"]))
+    if sha != kernel_sources_sha16():
+        return {}, f"{COUNTERS_SUMMARY.name} was measured on a library built from other sources"
+    return out, f"profiles/{COUNTERS_SUMMARY.name} (sha16 {sha})"
 
 
 def profile_kernel(args):
@@ -516,6 +541,7 @@ def profile_counters(args):
     torch.cuda.set_device(dev)
     plugin.load_table(args.table)
     gen = torch.Generator(device=dev).manual_seed(0)
+    print(json.dumps({"group": "meta", "kernel_sources_sha16": kernel_sources_sha16()}), flush=True)
     n = 5
     for name, N, Kd in SHAPES:
         w = (torch.randn(N, Kd, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
@@ -582,8 +608,9 @@ def floors(args):
 
     lib = ctypes.CDLL(str(FLOORS_LIB))
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
-    lib.vxf_stream.argtypes = [vp, i64, i64, i32, i32, i32, vp, vp, vp]
-    lib.vxf_pages.argtypes = [vp, i64, vp, i32, i32, i32, vp, vp, vp]
+    lib.vxf_stream.argtypes = [vp, i64, i64, i32, i32, i32, i32, vp, vp, vp]
+    lib.vxf_pages.argtypes = [vp, i64, vp, i32, i32, i32, i32, vp, vp, vp]
+    lib.vxf_wave_pages.argtypes = [vp, i64, vp, i32, i32, i32, i32, vp, vp, vp]
     lib.vxf_l2.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp, vp]
     lib.vxf_lds.argtypes = [i32, i32, i32, vp, vp, vp]
     lib.vxf_mfma.argtypes = [i32, i32, i32, vp, vp, vp]
@@ -664,31 +691,34 @@ def floors(args):
     out["l2_load_16B"] = l2
     del l2buf
 
-    # Streaming reads at the sweep's weight sizes, timed like the GEMMs
+    # Streaming reads at the sweep's weight sizes, timed like the GEMMs, with nontemporal loads
+    # (what the GEMMs use for weights read once) and with the default cache policy
     sizes = {"o": 4096 * 4096 * 2, "qkv": 6144 * 4096 * 2, "down": 4096 * 12288 * 2, "gate_up": 24576 * 4096 * 2}
     stream_rows = []
     for name, nbytes in sizes.items():
         rot = rotations_for(nbytes)
         bufs = [torch.empty(nbytes, device=dev, dtype=torch.uint8) for _ in range(rot)]
-        best = None
-        for blocks in (256, 512, 1024):
-            for q in (4, 8):
-                per_wg = nbytes // blocks
-                per_wg -= per_wg % (16 * 512)
-                if per_wg <= 0:
-                    continue
+        for nt in (1, 0):
+            best = None
+            for blocks in (256, 512, 1024):
+                for q in (4, 8):
+                    per_wg = nbytes // blocks
+                    per_wg -= per_wg % (16 * 512)
+                    if per_wg <= 0:
+                        continue
 
-                def call(i, blocks=blocks, q=q, per_wg=per_wg):
-                    check(lib.vxf_stream(bufs[i].data_ptr(), nbytes, per_wg, blocks, 512, q, sink.data_ptr(),
-                                         cyc.data_ptr(), st()))
+                    def call(i, blocks=blocks, q=q, per_wg=per_wg, nt=nt):
+                        check(lib.vxf_stream(bufs[i].data_ptr(), nbytes, per_wg, blocks, 512, q, nt, sink.data_ptr(),
+                                             cyc.data_ptr(), st()))
 
-                us = time_graph(call, rotations=rot)
-                row = {"blocks": blocks, "loads_in_flight": q, "us": round(us, 2),
-                       "bytes_read": per_wg * blocks, "hbm_frac": round(per_wg * blocks / us / 1e3 / HBM_PEAK_GBS, 3)}
-                if best is None or row["us"] < best["us"]:
-                    best = row
-        stream_rows.append({"weights_of": name, "bytes": nbytes, "copies": rot, **best})
-        log("stream", stream_rows[-1])
+                    us = time_graph(call, rotations=rot)
+                    row = {"blocks": blocks, "loads_in_flight": q, "us": round(us, 2), "bytes_read": per_wg * blocks,
+                           "hbm_frac": round(per_wg * blocks / us / 1e3 / HBM_PEAK_GBS, 3)}
+                    if best is None or row["us"] < best["us"]:
+                        best = row
+            stream_rows.append({"weights_of": name, "bytes": nbytes, "copies": rot,
+                                "policy": "nontemporal" if nt else "default", **best})
+            log("stream", stream_rows[-1])
         del bufs
         torch.cuda.empty_cache()
     empty_us = time_graph(lambda i: check(lib.vxf_mfma(4, 1, 1, sink.data_ptr(), cyc.data_ptr(), st())))
@@ -703,17 +733,31 @@ def floors(args):
     perm = torch.randperm(npg, device=dev, generator=gen).to(torch.int32)
     assert int(perm.max()) < npg and int(perm.min()) >= 0
     pg = []
-    for blocks in (1024, 2048, 4096):
-        ppw = npg // blocks
-        for q in (1, 2, 4):
-            us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, q,
-                                                      sink.data_ptr(), cyc.data_ptr(), st())), blocks)
-            pg.append({"blocks": blocks, "pages_in_flight": q, "us": round(us, 1),
-                       "TBps": round(blocks * ppw * 8192 / us / 1e6, 2)})
-            log("pages", pg[-1])
+    for nt in (1, 0):
+        for blocks in (1024, 2048, 4096):
+            ppw = npg // blocks
+            for q in (1, 2, 4):
+                us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, q, nt,
+                                                          sink.data_ptr(), cyc.data_ptr(), st())), blocks)
+                pg.append({"policy": "nontemporal" if nt else "default", "blocks": blocks, "pages_in_flight": q,
+                           "us": round(us, 1), "TBps": round(blocks * ppw * 8192 / us / 1e6, 2)})
+                log("pages", pg[-1])
     out["permuted_8k_pages"] = pg
+    # one wave per page in the attention kernel's lane pattern, 4 workgroups of 4 waves per CU
+    # (36 KiB of LDS each), as the attention kernel runs at 4 waves per SIMD
+    wp = []
+    for nt in (1, 0):
+        for blocks in (1024, 2048):
+            ppw = npg // (blocks * 4)
+            assert blocks * 4 * ppw <= npg
+            us, _ = timed(lambda: check(lib.vxf_wave_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, nt,
+                                                           36 * 1024, sink.data_ptr(), cyc.data_ptr(), st())), blocks)
+            wp.append({"policy": "nontemporal" if nt else "default", "blocks": blocks, "us": round(us, 1),
+                       "TBps": round(blocks * 4 * ppw * 8192 / us / 1e6, 2)})
+            log("wave_pages", wp[-1])
+    out["permuted_8k_pages_one_wave_each_attention_lanes"] = wp
     seq = torch.arange(npg, device=dev, dtype=torch.int32)
-    us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, seq.data_ptr(), 2048, npg // 2048, 2,
+    us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, seq.data_ptr(), 2048, npg // 2048, 2, 1,
                                               sink.data_ptr(), cyc.data_ptr(), st())), 2048)
     out["sequential_8k_pages_TBps"] = round(nb / us / 1e6, 2)
     out["ghz_one_wave_per_simd_mfma"] = ghz
@@ -844,6 +888,15 @@ def main():
         del wc, wbs, b8
         torch.cuda.empty_cache()
     per_op = [per_op[(M, name)] for M, name, _, _ in ops]
+    # measured HBM traffic per launch, where the counter record matches these sources and cfg
+    op_traffic, op_traffic_note = read_op_traffic()
+    for r in per_op:
+        t = op_traffic.get((r["M"], r["op"]))
+        if t is not None and t[1] == r["cfg"]:
+            r["traffic_bytes"] = t[0]
+            r["traffic_over_algorithmic"] = round(t[0] / gemm_bytes(r["M"], r["N"], r["K"]), 3)
+        else:
+            r["traffic_bytes"] = None
 
     # dominant kernel: the GEMM with the largest share of the step, timed alone on its stream
     dom = max(per_op, key=lambda r: r["gemm_us"])
@@ -1048,6 +1101,7 @@ def main():
         "cpu_baseline": cpu,
         "bit_exact": exact_ok,
         "per_op": per_op,
+        "per_op_traffic_source": op_traffic_note,
         "per_op_f15": per_op_f15,
         "config1": cfg1,
         "attention": attn,

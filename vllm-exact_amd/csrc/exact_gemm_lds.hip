@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void exact_lds_kernel(ExactParams p) {
   __shared__ __attribute__((aligned(1024))) int8_t ring[S * NF * 1024];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int wm = wave & 1, wn = wave >> 1;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
@@ -47,12 +47,18 @@ __global__ __launch_bounds__(256) void exact_lds_kernel(ExactParams p) {
   const int64_t ke = min(kb + p.kch, PACKED ? p.kpad : p.K);
   const int64_t nk = (ke - kb) >> 6;
 
-  // Global source of each fragment this wave loads (rows clamped into the matrices).
+  // Global source of each fragment this wave loads (rows clamped into the matrices). With a
+  // single M tile every weight byte is read by one workgroup only, so weight fragments are
+  // streamed with nontemporal loads; x fragments, which every N tile reads, keep the default
+  // policy so that they stay in L2.
+  const bool stream_w = cdiv<int64_t>(p.M, BM) == 1;
   const int8_t* src[LPW];
   int dst[LPW];
+  bool nt[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
     const int f = wave + 4 * i;
+    nt[i] = stream_w && f >= 2 * FX;
     if constexpr (PACKED) {
       // packed: fragment (tile, kt, plane) is 1 KiB of contiguous memory in lane order
       if (f < 2 * FX) {
@@ -80,9 +86,14 @@ __global__ __launch_bounds__(256) void exact_lds_kernel(ExactParams p) {
 
   auto issue = [&](int64_t step, int slot) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i)
-      __builtin_amdgcn_global_load_lds((void*)(src[i] + step * kStep), (lds_void_t*)(ring + slot * NF * 1024 + dst[i]),
-                                       16, 0, 0);
+    for (int i = 0; i < LPW; ++i) {
+      void* g = (void*)(src[i] + step * kStep);
+      lds_void_t* l = (lds_void_t*)(ring + slot * NF * 1024 + dst[i]);
+      if (nt[i])
+        __builtin_amdgcn_global_load_lds(g, l, 16, 0, 2);  // cache policy: nt
+      else
+        __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+    }
   };
 
   v4i hh[TM][TN], md[TM][TN], ll[TM][TN];

@@ -11,7 +11,8 @@
 // tiles x 2 digit planes, 1 KiB each in MFMA lane order) go through a two-slot LDS ring filled
 // by global_load_lds_dwordx4 (gfx950 direct-to-LDS loads) split over all waves; a wave whose
 // share does not divide evenly copies some fragment twice (the same bytes to the same place).
-// A wave's weight fragments of its two steps go to two register sets. Every load is issued from
+// A wave's weight fragments of its two steps go to two register sets (loaded nontemporal when the
+// grid has a single M tile, NTW: then no other workgroup reads them). Every load is issued from
 // inline asm and every wait is explicit, in one fixed order per round:
 //
 //   wait x(r) -> s_barrier -> wait W0(r) -> step 0, the x copies of round r + 1 (into the slot
@@ -56,7 +57,7 @@ constexpr int xk_lds_bytes(int bm, int bn, int kg, int nacc) {
 // terms), or lane-by-lane stores of any output (fp32, split-K partials, F = 15).
 enum XkOut { kOutBf16 = 0, kOutF16 = 1, kOutWide = 2 };
 
-template <int BM, int NWN, int WN, int KG, bool TRUNC, int OUT>
+template <int BM, int NWN, int WN, int KG, bool TRUNC, int OUT, bool NTW>
 __global__ __launch_bounds__(64 * NWN * KG) void exact_xk_kernel(ExactParams p) {
   constexpr int NWAVE = NWN * KG;
   constexpr int TM = BM / 16;          // 16-row tiles (every wave covers all of them)
@@ -162,7 +163,10 @@ __global__ __launch_bounds__(64 * NWN * KG) void exact_xk_kernel(ExactParams p) 
   auto issue_w = [&](int round, int s, v4i (&wb)[LW], int f) {
     const int step = min((round * KG + kg) * kSteps + s, nk - 1);
     const int8_t* base = wsrc[f >> 1] + step * 2048 + (f & 1) * 1024;
-    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(wb[f]) : "v"(voff), "s"(base) : "memory");
+    if constexpr (NTW)
+      asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=v"(wb[f]) : "v"(voff), "s"(base) : "memory");
+    else
+      asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(wb[f]) : "v"(voff), "s"(base) : "memory");
   };
 
   v4i acc[NACC][TM][TN];
@@ -377,13 +381,23 @@ hipError_t launch(const ExactParams& ep, hipStream_t st) {
   if (blocks * ep.sk > 0x7FFFFFFFLL || ep.sk > 65535) return hipErrorInvalidConfiguration;
   const dim3 grid((unsigned)blocks, (unsigned)ep.sk), block(64 * NWN * KG);
   const bool staged = ep.sk == 1 && ep.out_dtype != VXA_F32 && !ep.offset;
+  // One M tile: every weight byte is read by one workgroup, so weights are streamed with
+  // nontemporal loads. Several M tiles read the same weight tile close together (XCD swizzle)
+  // and should find it in L2.
+  const bool ntw = cdiv<int64_t>(ep.M, BM) == 1;
+#define VXA_XK_LAUNCH(OUT_)                                                                             \
+  if (ntw)                                                                                             \
+    hipLaunchKernelGGL((exact_xk_kernel<BM, NWN, WN, KG, TRUNC, OUT_, true>), grid, block, 0, st, ep);  \
+  else                                                                                                 \
+    hipLaunchKernelGGL((exact_xk_kernel<BM, NWN, WN, KG, TRUNC, OUT_, false>), grid, block, 0, st, ep);
   if (staged && ep.out_dtype == VXA_BF16) {
-    hipLaunchKernelGGL((exact_xk_kernel<BM, NWN, WN, KG, TRUNC, kOutBf16>), grid, block, 0, st, ep);
+    VXA_XK_LAUNCH(kOutBf16)
   } else if (staged) {
-    hipLaunchKernelGGL((exact_xk_kernel<BM, NWN, WN, KG, TRUNC, kOutF16>), grid, block, 0, st, ep);
+    VXA_XK_LAUNCH(kOutF16)
   } else {
-    hipLaunchKernelGGL((exact_xk_kernel<BM, NWN, WN, KG, TRUNC, kOutWide>), grid, block, 0, st, ep);
+    VXA_XK_LAUNCH(kOutWide)
   }
+#undef VXA_XK_LAUNCH
   return hipGetLastError();
 }
 

@@ -4,7 +4,10 @@
 // beside the published peak.
 //
 //   stream   contiguous read of a large buffer, one chunk per workgroup (the weight stream)
-//   pages    read of 8 KiB pages in a given (permuted) order (the paged KV stream)
+//   pages    read of 8 KiB pages in a given (permuted) order (the paged KV stream): a
+//            workgroup reads a page at a time, or (wave_pages) each wave reads its own pages
+//            in the decode attention kernel's lane pattern
+// The stream and page probes take the load's cache policy: nontemporal or the default.
 //   l2       16-byte loads of an L2-resident buffer into VGPRs, or straight into LDS with
 //            global_load_lds_dwordx4, at Q loads in flight per lane
 //   lds      ds_read_b128 of LDS into VGPRs
@@ -32,7 +35,13 @@ __device__ inline void finish(int* sink, int64_t* cycles, v4i acc, int64_t t0) {
 // Workgroup b reads bytes [b * per_wg, (b + 1) * per_wg): Q 16-byte non-temporal loads per lane
 // in flight, then the remainder one load per lane at a time. per_wg is a multiple of
 // 16 * blockDim.x (host-checked).
-template <int Q>
+template <bool NT>
+__device__ inline v4i load16(const v4i* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  return *p;
+}
+
+template <int Q, bool NT>
 __global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf, int64_t per_wg16, int* sink,
                                                      int64_t* cycles) {
   const int64_t t0 = clock64();
@@ -43,17 +52,17 @@ __global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf
   for (; i + (Q - 1) * T < per_wg16; i += T * Q) {
     v4i a[Q];
 #pragma unroll
-    for (int u = 0; u < Q; ++u) a[u] = __builtin_nontemporal_load(p + i + u * T);
+    for (int u = 0; u < Q; ++u) a[u] = load16<NT>(p + i + u * T);
 #pragma unroll
     for (int u = 0; u < Q; ++u) acc ^= a[u];
   }
-  for (; i < per_wg16; i += T) acc ^= __builtin_nontemporal_load(p + i);
+  for (; i < per_wg16; i += T) acc ^= load16<NT>(p + i);
   finish(sink, cycles, acc, t0);
 }
 
 // Workgroup b reads pages pages[b * ppw .. (b + 1) * ppw) of 8 KiB each; the 512 lanes of a
 // workgroup cover one page per round (one 16-byte load each), Q pages in flight.
-template <int Q>
+template <int Q, bool NT>
 __global__ __launch_bounds__(512) void pages_kernel(const v4i* __restrict__ buf, const int32_t* __restrict__ pages,
                                                     int ppw, int* sink, int64_t* cycles) {
   const int64_t t0 = clock64();
@@ -62,10 +71,40 @@ __global__ __launch_bounds__(512) void pages_kernel(const v4i* __restrict__ buf,
   for (int i = 0; i < ppw; i += Q) {
     v4i a[Q];
 #pragma unroll
-    for (int u = 0; u < Q; ++u) a[u] = __builtin_nontemporal_load(buf + (int64_t)mine[i + u] * 512 + threadIdx.x);
+    for (int u = 0; u < Q; ++u) a[u] = load16<NT>(buf + (int64_t)mine[i + u] * 512 + threadIdx.x);
 #pragma unroll
     for (int u = 0; u < Q; ++u) acc ^= a[u];
   }
+  finish(sink, cycles, acc, t0);
+}
+
+// Wave w of workgroup b reads pages pages[(4b + w) * ppw ..) of 8 KiB, one at a time, as the
+// decode attention reads a 16-key page of one KV head (16 rows of 512 bytes: K then V, D = 128):
+// four K loads with lane (r, c) on row c, bytes 64i + 16r, then four V loads with lane (r, c)
+// on row 4r + j, bytes 256 + 16c. 256 threads; `pad` bytes of dynamic LDS per workgroup cap
+// the workgroups per CU the way the attention kernel's registers do.
+template <bool NT>
+__global__ __launch_bounds__(256) void wave_pages_kernel(const int8_t* __restrict__ buf,
+                                                         const int32_t* __restrict__ pages, int ppw, int pad,
+                                                         int* sink, int64_t* cycles) {
+  extern __shared__ int lds_pad[];
+  const int64_t t0 = clock64();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 4, c = lane & 15;
+  const int32_t* mine = pages + ((int64_t)blockIdx.x * 4 + wave) * ppw;
+  v4i acc = {0, 0, 0, 0};
+  for (int i = 0; i < ppw; ++i) {
+    const int8_t* pg = buf + (int64_t)mine[i] * 8192;
+    v4i a[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = load16<NT>(reinterpret_cast<const v4i*>(pg + c * 512 + 64 * k + 16 * r));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[4 + j] = load16<NT>(reinterpret_cast<const v4i*>(pg + (4 * r + j) * 512 + 256 + 16 * c));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc ^= a[k];
+  }
+  if (pad) lds_pad[threadIdx.x] = acc.x;
   finish(sink, cycles, acc, t0);
 }
 
@@ -146,8 +185,8 @@ __global__ __launch_bounds__(1024) void mfma_kernel(int rounds, int* sink, int64
 extern "C" {
 
 // Status: 0 ok, 1 bad argument, 4 launch error.
-int vxf_stream(const void* buf, int64_t buf_bytes, int64_t per_wg_bytes, int blocks, int threads, int q, int* sink,
-               int64_t* cycles, void* stream) {
+int vxf_stream(const void* buf, int64_t buf_bytes, int64_t per_wg_bytes, int blocks, int threads, int q, int nt,
+               int* sink, int64_t* cycles, void* stream) {
   if (!buf || !sink || !cycles || blocks <= 0 || (threads != 256 && threads != 512)) return 1;
   if (q != 4 && q != 8) return 1;
   if (per_wg_bytes <= 0 || per_wg_bytes % (16LL * threads) != 0) return 1;
@@ -155,23 +194,50 @@ int vxf_stream(const void* buf, int64_t buf_bytes, int64_t per_wg_bytes, int blo
   const hipStream_t st = (hipStream_t)stream;
   const int64_t n16 = per_wg_bytes / 16;
   const auto* p = (const v4i*)buf;
-  if (q == 4) hipLaunchKernelGGL(stream_kernel<4>, dim3(blocks), dim3(threads), 0, st, p, n16, sink, cycles);
-  else if (q == 8) hipLaunchKernelGGL(stream_kernel<8>, dim3(blocks), dim3(threads), 0, st, p, n16, sink, cycles);
-  else return 1;
+#define VXF_STREAM(Q_, NT_) hipLaunchKernelGGL((stream_kernel<Q_, NT_>), dim3(blocks), dim3(threads), 0, st, p, n16, sink, cycles)
+  if (q == 4 && nt) VXF_STREAM(4, true);
+  else if (q == 8 && nt) VXF_STREAM(8, true);
+  else if (q == 4) VXF_STREAM(4, false);
+  else VXF_STREAM(8, false);
+#undef VXF_STREAM
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
 // pages: int32 [blocks * ppw] page indices, each in [0, buf_bytes / 8192) (the caller checks).
-int vxf_pages(const void* buf, int64_t buf_bytes, const int32_t* pages, int blocks, int ppw, int q, int* sink,
+int vxf_pages(const void* buf, int64_t buf_bytes, const int32_t* pages, int blocks, int ppw, int q, int nt, int* sink,
               int64_t* cycles, void* stream) {
   if (q != 1 && q != 2 && q != 4) return 1;
   if (!buf || !pages || !sink || !cycles || blocks <= 0 || ppw <= 0 || ppw % q != 0 || buf_bytes < 8192) return 1;
   const hipStream_t st = (hipStream_t)stream;
   const auto* p = (const v4i*)buf;
-  if (q == 1) hipLaunchKernelGGL(pages_kernel<1>, dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles);
-  else if (q == 2) hipLaunchKernelGGL(pages_kernel<2>, dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles);
-  else if (q == 4) hipLaunchKernelGGL(pages_kernel<4>, dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles);
-  else return 1;
+#define VXF_PAGES(Q_, NT_) hipLaunchKernelGGL((pages_kernel<Q_, NT_>), dim3(blocks), dim3(512), 0, st, p, pages, ppw, sink, cycles)
+  if (nt) {
+    if (q == 1) VXF_PAGES(1, true);
+    else if (q == 2) VXF_PAGES(2, true);
+    else VXF_PAGES(4, true);
+  } else {
+    if (q == 1) VXF_PAGES(1, false);
+    else if (q == 2) VXF_PAGES(2, false);
+    else VXF_PAGES(4, false);
+  }
+#undef VXF_PAGES
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// wave_pages: pages int32 [blocks * 4 * ppw], each in [0, buf_bytes / 8192) (the caller
+// checks); pad_bytes of dynamic LDS per workgroup, 0 or 1024 .. 65536.
+int vxf_wave_pages(const void* buf, int64_t buf_bytes, const int32_t* pages, int blocks, int ppw, int nt,
+                   int pad_bytes, int* sink, int64_t* cycles, void* stream) {
+  if (!buf || !pages || !sink || !cycles || blocks <= 0 || ppw <= 0 || buf_bytes < 8192) return 1;
+  if (pad_bytes != 0 && (pad_bytes < 1024 || pad_bytes > 65536)) return 1;
+  const hipStream_t st = (hipStream_t)stream;
+  const auto* p = (const int8_t*)buf;
+  if (nt)
+    hipLaunchKernelGGL(wave_pages_kernel<true>, dim3(blocks), dim3(256), pad_bytes, st, p, pages, ppw, pad_bytes, sink,
+                       cycles);
+  else
+    hipLaunchKernelGGL(wave_pages_kernel<false>, dim3(blocks), dim3(256), pad_bytes, st, p, pages, ppw, pad_bytes,
+                       sink, cycles);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
