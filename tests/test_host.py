@@ -125,6 +125,34 @@ def test_bench_traffic_is_tied_to_cfg_and_sources(tmp_path, monkeypatch):
     assert traffic is None and "other sources" in why
 
 
+def test_bench_per_op_traffic_is_tied_to_sources(tmp_path, monkeypatch):
+    # bench.py attaches a per-op traffic figure from the counter record only when the record
+    # was measured on a library built from the current sources
+    import importlib.util
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("bench_mod2", root / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    summary = tmp_path / "counters.md"
+    monkeypatch.setattr(bench, "COUNTERS_SUMMARY", summary)
+
+    def write(sha_):
+        summary.write_text("# counters\n\n| table |\n\n"
+                           f"    kernel_sources_sha16 = {sha_}\n"
+                           "    traffic M:1 op:qkv cfg:[16,32,128,16,1,8,1] = 50960000\n"
+                           "    traffic M:256 op:down cfg:[128,128,128,8,2,8,4] = 182931202\n")
+
+    write(bench.kernel_sources_sha16())
+    got, src = bench.read_op_traffic()
+    assert got == {(1, "qkv"): (50960000, [16, 32, 128, 16, 1, 8, 1]),
+                   (256, "down"): (182931202, [128, 128, 128, 8, 2, 8, 4])}
+    assert bench.kernel_sources_sha16() in src
+    write("0" * 16)
+    got, why = bench.read_op_traffic()
+    assert got == {} and "other sources" in why
+
+
 def test_bench_refuses_more_than_one_gpu():
     import subprocess
     from pathlib import Path
