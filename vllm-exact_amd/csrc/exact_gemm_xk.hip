@@ -403,7 +403,7 @@ hipError_t launch(const ExactParams& ep, hipStream_t st) {
 
 // Instantiated (BM, NWN, WN, KG, 4-dot too), 8 waves: cfg (BM, NWN * WN, 64 * KG, 8, 2).
 #define VXA_XK_TABLE(X) \
-  X(128, 4, 48, 2, 0) X(128, 4, 32, 2, 0) X(64, 2, 48, 4, 1) X(64, 2, 32, 4, 1) X(64, 4, 32, 2, 1) X(64, 4, 48, 2, 1)
+  X(128, 4, 48, 2, 0) X(128, 4, 32, 2, 1) X(64, 2, 48, 4, 1) X(64, 2, 32, 4, 1) X(64, 4, 32, 2, 1) X(64, 4, 48, 2, 1)
 
 template <bool TRUNC>
 hipError_t dispatch(const ExactPlan& pl, const ExactParams& ep, hipStream_t st) {

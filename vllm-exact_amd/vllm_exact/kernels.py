@@ -274,7 +274,7 @@ XW_SHAPES = [(32, 128, 4, 4), (32, 256, 4, 4), (64, 64, 4, 4), (64, 128, 4, 4), 
              (128, 192, 3, 8), (128, 192, 4, 8), (128, 256, 2, 8), (64, 96, 4, 6), (64, 96, 6, 6), (64, 96, 8, 6),
              (64, 96, 4, 3), (64, 96, 6, 3)]  # (BM, BN, weight sets, waves); BK = 64
 XK_SHAPES = [(128, 192, 2), (128, 128, 2), (64, 96, 4), (64, 64, 4), (64, 128, 2), (64, 192, 2)]  # (BM, BN, KG)
-XK_FOUR_DOTS = [(64, 96, 4), (64, 64, 4), (64, 128, 2), (64, 192, 2)]  # the shapes with 4-dot instantiations
+XK_FOUR_DOTS = [(128, 128, 2), (64, 96, 4), (64, 64, 4), (64, 128, 2), (64, 192, 2)]  # the shapes with 4-dot instantiations
 EXACT_CFGS = ([(16 * mt, 16 * nt, 128, nwk, c, 8) for mt, nt, c, nwk in SMALL_SHAPES]
               + [(bm, bn, 128, 4, st, 8) for bm, bn, st in LDS_SHAPES]
               + [(bm, bn, 64, nw, r, 8) for bm, bn, r, nw in XW_SHAPES]
