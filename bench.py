@@ -27,7 +27,9 @@ Also reported, from the same run:
   64/8K and 16/16K: ms per step as a HIP graph, the same step with hipBLASLt bf16 linears,
   for each leg the time of its linears, attention calls and glue each in a graph of its own,
   bitwise batch invariance of the logits, and a CPU estimate from the oracle's timings;
-* bit-exactness of the benchmarked outputs against the CPU oracle (sampled rows);
+* bit-exactness against the CPU oracle: `bit_exact` on every per_op and per_op_f15 row
+  (output rows 0..7, M/2 and M-1 of the op as timed), and on the line, all of them with
+  lm_head's sampled rows and config 1's whole outputs (`bit_exact_scope` says which);
 * `per_op_f15`: the 4-dot variant, the same sweep at F = 15 (offset digits) with the table
   tuned at F = 15, on weights packed at F = 15;
 * `config1`: M = 16, K = N = 4096, F = 14 with all four dots and no split-K: GEMM and op
@@ -238,10 +240,21 @@ def roof_fields(M, N, Kd, t_us, ndots):
                 bound="hbm" if b / (HBM_PEAK_GBS * 1e9) >= o / (INT8_PEAK_TOPS * 1e12) else "mfma")
 
 
-def sweep_f15(torch, K, plugin, weights, xs, table_f15, table_f14):
+def sampled_rows_exact(torch, np, oracle, x, wd, y, Fx, trunc):
+    """True when the bf16 output rows 0..7, M/2 and M-1 of y = exactmm::linear(x, w) equal,
+    bit for bit, the oracle's result on the same rows (wd: the oracle's digits of w at Fx)."""
+    M = x.shape[0]
+    rows = np.unique(np.concatenate([np.arange(min(M, 8)), [M // 2, M - 1]]))
+    ref = oracle.exact_linear_c(oracle.digitize_c(x.float().cpu().numpy()[rows], Fx), wd, Fx, trunc)
+    got = y[rows.tolist()].cpu().view(torch.int16).numpy().view(np.uint16)
+    return bool(np.array_equal(got, oracle.bf16_rne_c(ref).reshape(ref.shape)))
+
+
+def sweep_f15(torch, K, plugin, weights, xs, table_f15, table_f14, np, oracle):
     """The 4-dot variant: the sweep at F = 15 (offset digits, the reference's "f=15, 4 dots")
     with the table tuned at F = 15, each op through exactmm::linear on weights packed at
-    F = 15, timed like the F = 14 sweep. Restores F = 14 and its table afterwards."""
+    F = 15, timed like the F = 14 sweep and its sampled output rows checked bitwise against
+    the oracle. Restores F = 14 and its table afterwards."""
     from vllm_exact.graph_timing import rotations_for
 
     recs = []
@@ -252,11 +265,14 @@ def sweep_f15(torch, K, plugin, weights, xs, table_f15, table_f14):
             w = weights[name + ".bf16"]
             wp = plugin.pack_weight(w)
             wc = [wp] + [tuple(t.clone() for t in wp) for _ in range(max(3, rotations_for(2 * N * Kd)) - 1)]
+            wd = oracle.digitize_c(w.float().cpu().numpy(), 15)
             for M in MS:
                 cfg = plugin._cfg(M, N, Kd)
                 t_op, t_gemm, one = time_op_and_gemm(torch, K, plugin, xs[(M, Kd)], wc, N, Kd, 15, False, cfg)
+                exact = sampled_rows_exact(torch, np, oracle, xs[(M, Kd)], wd,
+                                           torch.ops.exactmm.linear(xs[(M, Kd)], *wc[0]), 15, False)
                 rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
-                           one_launch=one, **roof_fields(M, N, Kd, t_gemm, 4))
+                           one_launch=one, bit_exact=exact, **roof_fields(M, N, Kd, t_gemm, 4))
                 recs.append(rec)
                 log("f15", json.dumps(rec))
             del wc, wp
@@ -858,8 +874,12 @@ def main():
     # ---------------------------------------------------------------- per-op detail
     # Each shape is timed on enough weight copies that one rotation streams >= 768 MB, past
     # the 256 MB MALL (three copies of a small shape would stay in it).
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle  # CPU oracle: checks the outputs, never computes them
+
     per_op = {}
     for name, N, Kd in SHAPES:
+        wd = oracle.digitize_c(weights[name + ".bf16"].float().cpu().numpy(), F)
         nrot = max(rot, rotations_for(2 * N * Kd))
         wc = weights[name] + [tuple(t.clone() for t in weights[name][0]) for _ in range(nrot - rot)]
         wbs = [weights[name + ".bf16"].clone() for _ in range(rotations_for(2 * N * Kd))]
@@ -882,7 +902,8 @@ def main():
             rec = dict(M=M, op=name, N=N, K=Kd, cfg=list(cfg), op_us=round(t_op, 2), gemm_us=round(t_gemm, 2),
                        bf16_hipblaslt_us=round(t_bf16, 2), int8_1dot_vendor_us=t_i8,
                        **roof_fields(M, N, Kd, t_gemm, NDOTS),
-                       vs_bf16=round(t_op / t_bf16, 2), weight_copies=nrot, one_launch=one_launch)
+                       vs_bf16=round(t_op / t_bf16, 2), weight_copies=nrot, one_launch=one_launch,
+                       bit_exact=sampled_rows_exact(torch, np, oracle, x, wd, op_call(M, name, Kd, 0), F, TRUNC))
             per_op[(M, name)] = rec
             log(json.dumps(rec))
         del wc, wbs, b8
@@ -928,25 +949,14 @@ def main():
     log("roofline:", json.dumps(roof))
 
     # ---------------------------------------------------------------- bit-exactness of the outputs
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import oracle  # CPU oracle: checks the outputs, never computes them
-
-    exact_ok = True
-    for M, name, N, Kd in [(16, "o", 4096, 4096), (256, "down", 4096, 12288), (1, "qkv", 6144, 4096)]:
-        y = op_call(M, name, Kd, 0).float().cpu().numpy()
-        wd = oracle.digitize_c(weights[name + ".bf16"].float().cpu().numpy(), F)
-        rows = np.arange(min(M, 8))
-        xdn = oracle.digitize_c(xs[(M, Kd)].float().cpu().numpy()[rows], F)
-        ref = oracle.exact_linear_c(xdn, wd, F, TRUNC)
-        want = oracle.bf16_rne_c(ref).reshape(ref.shape)
-        got = torch.from_numpy(y[rows]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
-        exact_ok &= bool(np.array_equal(got, want))
+    # every op of the sweep, on its sampled rows (rows 0..7, M/2 and M-1)
+    exact_ok = all(r["bit_exact"] for r in per_op)
     log("bit-exact vs oracle:", exact_ok)
 
     # ---------------------------------------------------------------- 4 dots: F = 15 sweep, config 1
     per_op_f15, cfg1 = [], None
     if not args.no_f15:
-        per_op_f15 = sweep_f15(torch, K, plugin, weights, xs, args.table_f15, args.table)
+        per_op_f15 = sweep_f15(torch, K, plugin, weights, xs, args.table_f15, args.table, np, oracle)
         cfg1 = config1(torch, K, plugin, oracle, np, dev, gen)
 
     # ---------------------------------------------------------------- attention
@@ -1099,7 +1109,11 @@ def main():
                    "step_TOPS": round(step_ops / (step_ms * 1e-3) / 1e12, 2)},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "bit_exact": exact_ok,
+        "bit_exact": exact_ok and all(r["bit_exact"] for r in per_op_f15 + lm_head)
+        and (cfg1 is None or cfg1["bit_exact_fp32_bf16"]),
+        "bit_exact_scope": "sampled output rows (0..7, M/2, M-1) of every per_op and per_op_f15 op, rows 0, "
+                           "M/2, M-1 of lm_head (first 4096 columns), all of config1 (fp32 and bf16), against the "
+                           "CPU oracle",
         "per_op": per_op,
         "per_op_traffic_source": op_traffic_note,
         "per_op_f15": per_op_f15,
