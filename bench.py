@@ -613,7 +613,8 @@ def floors(args):
     the probe kernels of vllm-exact_amd/floors/floors.hip (which compute nothing useful). Each
     kernel-timed figure is one launch timed with HIP events on torch's stream; the streaming
     reads at the sweep's weight sizes are timed like the GEMMs (graph replay, buffers rotated
-    past the MALL). The shader clock comes from s_memtime cycles over event time."""
+    past the MALL). Each probe's shader clock is its workgroups' s_memtime cycles over their
+    s_memrealtime ticks (100 MHz)."""
     import ctypes
     import hashlib
     import statistics
@@ -635,7 +636,7 @@ def floors(args):
     ncu = torch.cuda.get_device_properties(dev).multi_processor_count
     max_blocks = 4096
     sink = torch.zeros(max_blocks * 1024, device=dev, dtype=torch.int32)
-    cyc = torch.zeros(max_blocks, device=dev, dtype=torch.int64)
+    cyc = torch.zeros(2 * max_blocks, device=dev, dtype=torch.int64)  # shader cycles, then 100 MHz ticks
 
     def st():
         return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -645,11 +646,12 @@ def floors(args):
             raise RuntimeError(f"floors probe refused its arguments or failed to launch (status {rc})")
 
     def timed(launch, blocks, reps=5):
-        """Median event time (us) of one launch and the mean shader cycles of its workgroups."""
+        """Median event time (us) of one launch, the mean shader cycles of its workgroups, and the
+        shader clock (GHz) they ran at: their s_memtime cycles over their s_memrealtime ticks."""
         assert blocks <= max_blocks
         launch()
         torch.cuda.synchronize()
-        us, cycles = [], []
+        us, cycles, ghz = [], [], []
         for _ in range(reps):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
@@ -657,8 +659,10 @@ def floors(args):
             b.record()
             b.synchronize()
             us.append(a.elapsed_time(b) * 1000.0)
-            cycles.append(cyc[:blocks].double().mean().item())
-        return statistics.median(us), statistics.median(cycles)
+            c = cyc[:2 * blocks].double().view(2, blocks)
+            cycles.append(c[0].mean().item())
+            ghz.append(c[0].sum().item() / c[1].sum().item() * 0.1)
+        return statistics.median(us), statistics.median(cycles), statistics.median(ghz)
 
     out = {"mode": "floors", "cus": ncu, "source_sha16": hashlib.sha256(FLOORS_SRC.read_bytes()).hexdigest()[:16]}
 
@@ -666,27 +670,25 @@ def floors(args):
     mf = []
     for waves in (4, 8, 16):
         rounds = 4096
-        us, cy = timed(lambda: check(lib.vxf_mfma(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())), ncu)
+        us, _, ghz_run = timed(lambda: check(lib.vxf_mfma(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())),
+                               ncu)
         per_simd = rounds * 8 * waves / 4
         ops = ncu * waves * rounds * 8 * 16 * 16 * 64 * 2
-        mf.append({"waves_per_cu": waves, "us": round(us, 1), "ghz": round(cy / us / 1e3, 3),
-                   "cycles_per_mfma_per_simd": round(cy / per_simd, 2), "TOPS": round(ops / us / 1e6, 1)})
+        mf.append({"waves_per_cu": waves, "us": round(us, 1), "ghz": round(ghz_run, 3),
+                   "cycles_per_mfma_per_simd": round(us * 1e3 * ghz_run / per_simd, 2), "TOPS": round(ops / us / 1e6, 1)})
         log("mfma", mf[-1])
     out["mfma_i8_16x16x64"] = mf
-    # with one wave per SIMD the first wave's cycles span the whole workgroup; with more, a
-    # wave can finish before the others, so its cycle count says nothing about the clock
     ghz = mf[0]["ghz"]
-    for r in mf[1:]:
-        r.pop("ghz")
-        r.pop("cycles_per_mfma_per_simd")
 
     # LDS reads: ds_read_b128, 8 in flight per lane
     ld = []
     for waves in (4, 8, 16):
         rounds = 2048
-        us, cy = timed(lambda: check(lib.vxf_lds(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())), ncu)
+        us, _, ghz_run = timed(lambda: check(lib.vxf_lds(waves, ncu, rounds, sink.data_ptr(), cyc.data_ptr(), st())),
+                               ncu)
         b = rounds * 8 * 64 * 16 * waves
-        ld.append({"waves_per_cu": waves, "us": round(us, 1), "bytes_per_clk_per_cu": round(b / (us * 1e3 * ghz), 1)})
+        ld.append({"waves_per_cu": waves, "us": round(us, 1), "ghz": round(ghz_run, 3),
+                   "bytes_per_clk_per_cu": round(b / (us * 1e3 * ghz_run), 1)})
         log("lds", ld[-1])
     out["lds_read_b128"] = ld
 
@@ -697,14 +699,60 @@ def floors(args):
         for waves in (4, 8, 16):
             for q in (1, 2, 4, 8):
                 rounds = max(64, 16384 // (q * waves))
-                us, cy = timed(lambda: check(lib.vxf_l2(l2buf.data_ptr(), l2buf.numel(), lds, q, waves, ncu, rounds,
-                                                        sink.data_ptr(), cyc.data_ptr(), st())), ncu)
+                us, _, ghz_run = timed(lambda: check(lib.vxf_l2(l2buf.data_ptr(), l2buf.numel(), lds, q, waves, ncu,
+                                                                rounds, sink.data_ptr(), cyc.data_ptr(), st())), ncu)
                 b = rounds * q * 1024 * waves
                 l2.append({"path": "lds" if lds else "vgpr", "waves_per_cu": waves, "loads_in_flight": q,
-                           "us": round(us, 1), "bytes_per_clk_per_cu": round(b / (us * 1e3 * ghz), 1),
+                           "us": round(us, 1), "ghz": round(ghz_run, 3),
+                           "bytes_per_clk_per_cu": round(b / (us * 1e3 * ghz_run), 1),
                            "TBps": round(b * ncu / us / 1e6, 2)})
                 log("l2", l2[-1])
     out["l2_load_16B"] = l2
+
+    # The shader clock under the large-M GEMM's mix: MFMAs with loads in about its proportion (56
+    # MFMAs per 8 KiB a wave loads: 146 bytes per MFMA per CU, where the M = 256 gate_up tile loads
+    # 2.62 MB per 18,432 MFMAs), the loads all L2-resident or a quarter of them streamed from HBM
+    # (a 1 GiB buffer, past the MALL), and under each part alone; the MFMA operands constant or
+    # redrawn every round (random bits, as the GEMM's digits). Three launches of about 1-2 ms back
+    # to back; the clock of the last, per workgroup, from s_memtime over s_memrealtime.
+    lib.vxf_mfma_mix.argtypes = [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp]
+    clk = torch.zeros(2 * ncu, device=dev, dtype=torch.int64)
+    hbuf = torch.empty(1 << 30, device=dev, dtype=torch.uint8)
+    under = []
+    for loads, mfmas, vary in ((1, 0, 0), (2, 0, 0), (0, 56, 0), (0, 56, 1), (1, 56, 0), (1, 56, 1), (2, 56, 0),
+                               (2, 56, 1)):
+        rounds = 2000
+
+        def launch(loads=loads, mfmas=mfmas, vary=vary):
+            check(lib.vxf_mfma_mix(l2buf.data_ptr(), l2buf.numel(), hbuf.data_ptr(), hbuf.numel(), loads, mfmas, vary,
+                                   ncu, rounds, sink.data_ptr(), clk.data_ptr(), st()))
+
+        launch()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(3):
+            launch()
+        b.record()
+        b.synchronize()
+        us = a.elapsed_time(b) * 1000.0 / 3
+        c = clk.view(-1, 2).double()
+        ghz_wg = (c[:, 0] / c[:, 1] * 0.1).cpu()
+        cycles = float(c[:, 0].median())
+        row = {"loads": ["none", "l2", "l2_and_hbm"][loads], "mfmas_per_8KiB": mfmas,
+               "mfma_operands": "random" if vary else "constant", "us": round(us, 1),
+               "ghz_median": round(float(ghz_wg.median()), 3), "ghz_min": round(float(ghz_wg.min()), 3),
+               "ghz_max": round(float(ghz_wg.max()), 3)}
+        if loads:
+            row["bytes_per_clk_per_cu"] = round(rounds * 8 * 8192 / cycles, 1)
+            if loads == 2:
+                row["hbm_TBps"] = round(ncu * rounds * 2 * 8192 / us / 1e6, 2)
+        if mfmas:
+            row["TOPS"] = round(ncu * 8 * rounds * mfmas * 16 * 16 * 64 * 2 / us / 1e6, 1)
+        under.append(row)
+        log("clock under load", row)
+    del hbuf
+    out["clock_under_gemm_mix"] = under
     del l2buf
 
     # Streaming reads at the sweep's weight sizes, timed like the GEMMs, with nontemporal loads
@@ -753,7 +801,7 @@ def floors(args):
         for blocks in (1024, 2048, 4096):
             ppw = npg // blocks
             for q in (1, 2, 4):
-                us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, q, nt,
+                us, _, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, q, nt,
                                                           sink.data_ptr(), cyc.data_ptr(), st())), blocks)
                 pg.append({"policy": "nontemporal" if nt else "default", "blocks": blocks, "pages_in_flight": q,
                            "us": round(us, 1), "TBps": round(blocks * ppw * 8192 / us / 1e6, 2)})
@@ -766,14 +814,14 @@ def floors(args):
         for blocks in (1024, 2048):
             ppw = npg // (blocks * 4)
             assert blocks * 4 * ppw <= npg
-            us, _ = timed(lambda: check(lib.vxf_wave_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, nt,
+            us, _, _ = timed(lambda: check(lib.vxf_wave_pages(pbuf.data_ptr(), nb, perm.data_ptr(), blocks, ppw, nt,
                                                            36 * 1024, sink.data_ptr(), cyc.data_ptr(), st())), blocks)
             wp.append({"policy": "nontemporal" if nt else "default", "blocks": blocks, "us": round(us, 1),
                        "TBps": round(blocks * 4 * ppw * 8192 / us / 1e6, 2)})
             log("wave_pages", wp[-1])
     out["permuted_8k_pages_one_wave_each_attention_lanes"] = wp
     seq = torch.arange(npg, device=dev, dtype=torch.int32)
-    us, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, seq.data_ptr(), 2048, npg // 2048, 2, 1,
+    us, _, _ = timed(lambda: check(lib.vxf_pages(pbuf.data_ptr(), nb, seq.data_ptr(), 2048, npg // 2048, 2, 1,
                                               sink.data_ptr(), cyc.data_ptr(), st())), 2048)
     out["sequential_8k_pages_TBps"] = round(nb / us / 1e6, 2)
     out["ghz_one_wave_per_simd_mfma"] = ghz

@@ -1,5 +1,5 @@
 """The probe library behind `bench.py --floors` (vllm-exact_amd/floors/floors.hip): it loads,
-exports its five probes, and refuses malformed arguments before launching anything (no GPU
+exports its six probes, and refuses malformed arguments before launching anything (no GPU
 needed: every refusal happens on the host)."""
 import ctypes
 from pathlib import Path
@@ -17,6 +17,7 @@ SIGS = {
     "vxf_l2": [vp, i64, i32, i32, i32, i32, i32, vp, vp, vp],
     "vxf_lds": [i32, i32, i32, vp, vp, vp],
     "vxf_mfma": [i32, i32, i32, vp, vp, vp],
+    "vxf_mfma_mix": [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp],
 }
 
 
@@ -53,3 +54,11 @@ def test_probes_refuse_malformed_arguments(lib):
     # l2: buffer not a power of two, unsupported wave count
     assert lib.vxf_l2(p, 3 << 20, 0, 4, 4, 1, 1, p, p, None) == 1
     assert lib.vxf_l2(p, 1 << 21, 0, 4, 5, 1, 1, p, p, None) == 1
+    # mfma_mix: neither loads nor MFMAs, an MFMA count not a multiple of 8, no clock buffer, HBM
+    # loads without a buffer or with less than 8 KiB per workgroup, an unknown operand mode
+    assert lib.vxf_mfma_mix(p, 1 << 21, p, 1 << 30, 0, 0, 0, 1, 1, p, p, None) == 1
+    assert lib.vxf_mfma_mix(p, 1 << 21, p, 1 << 30, 1, 12, 0, 1, 1, p, p, None) == 1
+    assert lib.vxf_mfma_mix(p, 1 << 21, p, 1 << 30, 1, 56, 0, 1, 1, p, None, None) == 1
+    assert lib.vxf_mfma_mix(p, 1 << 21, None, 1 << 30, 2, 56, 0, 1, 1, p, p, None) == 1
+    assert lib.vxf_mfma_mix(p, 1 << 21, p, 4096, 2, 56, 0, 1, 1, p, p, None) == 1
+    assert lib.vxf_mfma_mix(p, 1 << 21, p, 1 << 30, 1, 56, 2, 1, 1, p, p, None) == 1

@@ -12,11 +12,14 @@
 //            global_load_lds_dwordx4, at Q loads in flight per lane
 //   lds      ds_read_b128 of LDS into VGPRs
 //   mfma     v_mfma_i32_16x16x64_i8 on 8 independent accumulators per wave
+//   mfma_mix MFMAs and loads (L2-resident, or L2 and HBM) at once, in the large-M exact GEMM's
+//            proportion, with the shader clock each workgroup ran at
 //
 // Every kernel reads inside the buffer it is given (the host checks the sizes; the L2 probe
 // masks its offsets with a power of two that the buffer covers) and writes one int per thread
-// to `sink`, so no load can be optimised away. Thread 0 of each workgroup also writes the
-// shader-clock cycles its workgroup took, from which the host derives the clock rate.
+// to `sink`, so no load can be optimised away. Thread 0 of each workgroup b also writes the
+// shader cycles (s_memtime) and the 100 MHz ticks (s_memrealtime) of its run, at cycles[b] and
+// cycles[blocks + b]: their ratio is the shader clock the probe ran at.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -26,10 +29,20 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 namespace {
 
-__device__ inline void finish(int* sink, int64_t* cycles, v4i acc, int64_t t0) {
+// Start stamps of thread 0's run: shader cycles (s_memtime) and 100 MHz ticks (s_memrealtime).
+struct Stamp {
+  int64_t cycles, ticks;
+};
+__device__ inline Stamp stamp() { return {(int64_t)clock64(), (int64_t)__builtin_amdgcn_s_memrealtime()}; }
+
+__device__ inline void finish(int* sink, int64_t* cycles, v4i acc, Stamp t0) {
   // An impossible value keeps the loads live without a store per thread in the common case.
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5A5A5A5A) sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = 1;
-  if (threadIdx.x == 0) cycles[blockIdx.x] = (int64_t)clock64() - t0;
+  if (threadIdx.x == 0) {
+    const Stamp t1 = stamp();
+    cycles[blockIdx.x] = t1.cycles - t0.cycles;
+    cycles[gridDim.x + blockIdx.x] = t1.ticks - t0.ticks;
+  }
 }
 
 // Workgroup b reads bytes [b * per_wg, (b + 1) * per_wg): Q 16-byte non-temporal loads per lane
@@ -44,7 +57,7 @@ __device__ inline v4i load16(const v4i* p) {
 template <int Q, bool NT>
 __global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf, int64_t per_wg16, int* sink,
                                                      int64_t* cycles) {
-  const int64_t t0 = clock64();
+  const Stamp t0 = stamp();
   const v4i* p = buf + (int64_t)blockIdx.x * per_wg16;
   const int64_t T = blockDim.x;
   v4i acc = {0, 0, 0, 0};
@@ -65,7 +78,7 @@ __global__ __launch_bounds__(512) void stream_kernel(const v4i* __restrict__ buf
 template <int Q, bool NT>
 __global__ __launch_bounds__(512) void pages_kernel(const v4i* __restrict__ buf, const int32_t* __restrict__ pages,
                                                     int ppw, int* sink, int64_t* cycles) {
-  const int64_t t0 = clock64();
+  const Stamp t0 = stamp();
   const int32_t* mine = pages + (int64_t)blockIdx.x * ppw;
   v4i acc = {0, 0, 0, 0};
   for (int i = 0; i < ppw; i += Q) {
@@ -88,7 +101,7 @@ __global__ __launch_bounds__(256) void wave_pages_kernel(const int8_t* __restric
                                                          const int32_t* __restrict__ pages, int ppw, int pad,
                                                          int* sink, int64_t* cycles) {
   extern __shared__ int lds_pad[];
-  const int64_t t0 = clock64();
+  const Stamp t0 = stamp();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane >> 4, c = lane & 15;
@@ -115,7 +128,7 @@ template <int Q, bool LDS>
 __global__ __launch_bounds__(1024) void l2_kernel(const v4i* __restrict__ buf, int64_t mask16, int rounds, int* sink,
                                                   int64_t* cycles) {
   __shared__ __attribute__((aligned(1024))) int8_t ring[LDS ? 16 * Q * 1024 : 16];
-  const int64_t t0 = clock64();
+  const Stamp t0 = stamp();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t base = ((int64_t)blockIdx.x * 16 + wave) * 1024;  // in 16-byte units
@@ -149,7 +162,7 @@ __global__ __launch_bounds__(1024) void lds_kernel(int rounds, int* sink, int64_
   __shared__ __attribute__((aligned(1024))) int8_t tile[64 * 1024];
   for (int i = threadIdx.x; i < 4096; i += blockDim.x) reinterpret_cast<v4i*>(tile)[i] = v4i{i, i + 1, i + 2, i + 3};
   __syncthreads();
-  const int64_t t0 = clock64();
+  const Stamp t0 = stamp();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   v4i acc = {0, 0, 0, 0};
   for (int r = 0; r < rounds; ++r) {
@@ -165,7 +178,7 @@ __global__ __launch_bounds__(1024) void lds_kernel(int rounds, int* sink, int64_
 
 // v_mfma_i32_16x16x64_i8 on 8 independent accumulators per wave.
 __global__ __launch_bounds__(1024) void mfma_kernel(int rounds, int* sink, int64_t* cycles) {
-  const int64_t t0 = clock64();
+  const Stamp t0 = stamp();
   const v4i a = {(int)threadIdx.x, 3, 5, 7}, b = {11, 13, (int)blockIdx.x, 17};
   v4i c[8];
 #pragma unroll
@@ -178,6 +191,63 @@ __global__ __launch_bounds__(1024) void mfma_kernel(int rounds, int* sink, int64
 #pragma unroll
   for (int i = 1; i < 8; ++i) acc ^= c[i];
   finish(sink, cycles, acc, t0);
+}
+
+// MFMAs and loads together, the mix of the large-M exact GEMM: 8 waves per workgroup, one
+// workgroup per CU. Each round a wave issues eight 16-byte loads per lane (8 KiB) when
+// loads > 0: all from the L2-resident buffer `l2` (offsets masked into it), or with loads == 2
+// two of the eight from the workgroup's own chunk of the large buffer `hbm` (read round after
+// round, offsets masked into the chunk), then `mfmas` MFMAs over 8 independent chains, then
+// consumes the loads. With `vary`, the MFMA operands are redrawn every round (a 32-bit linear
+// congruential step per register: random bits, as the GEMM's digits are), else they stay
+// constant. Thread 0 records, for its workgroup, the shader cycles (s_memtime) and the
+// 100 MHz ticks (s_memrealtime) of the run: their ratio is the shader clock under that load.
+__global__ __launch_bounds__(512) void mfma_mix_kernel(const v4i* __restrict__ l2, int64_t mask16,
+                                                       const v4i* __restrict__ hbm, int64_t chunk16, int loads,
+                                                       int mfmas, int vary, int rounds, int* sink, int64_t* clk) {
+  const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t base = ((int64_t)blockIdx.x * 8 + wave) * 512;  // 16-byte units
+  const v4i* mine = hbm + (int64_t)blockIdx.x * (chunk16 + 1);
+  v4i a = {(int)threadIdx.x, 3, 5, 7}, b = {11, 13, (int)blockIdx.x, 17};
+  v4i c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = v4i{i, 0, 0, 0};
+  v4i acc = {0, 0, 0, 0};
+  for (int r = 0; r < rounds; ++r) {
+    if (vary) {
+      a = a * 1664525 + 1013904223;
+      b = b * 22695477 + 1;
+    }
+    v4i d[8];
+    if (loads) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (loads == 2 && u < 2)
+          d[u] = mine[((int64_t)(r * 2 + u) * 512 + wave * 64 + lane) & chunk16];
+        else
+          d[u] = l2[(base + (int64_t)(r * 8 + u) * 64 + lane) & mask16];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) d[u] = v4i{u, r, 0, 0};
+    }
+    for (int m = 0; m < mfmas; m += 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= d[u];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc ^= c[i];
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x5A5A5A5A) sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = 1;
+  if (threadIdx.x == 0) {
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    clk[2 * blockIdx.x] = (int64_t)(c1 - c0);
+    clk[2 * blockIdx.x + 1] = (int64_t)(r1 - r0);
+  }
 }
 
 }  // namespace
@@ -271,6 +341,28 @@ int vxf_lds(int waves, int blocks, int rounds, int* sink, int64_t* cycles, void*
 int vxf_mfma(int waves, int blocks, int rounds, int* sink, int64_t* cycles, void* stream) {
   if (!sink || !cycles || blocks <= 0 || rounds <= 0 || (waves != 4 && waves != 8 && waves != 16)) return 1;
   hipLaunchKernelGGL(mfma_kernel, dim3(blocks), dim3(64 * waves), 0, (hipStream_t)stream, rounds, sink, cycles);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// mfma_mix: l2_bytes a power of two >= 16 KiB; hbm_bytes >= blocks * chunk with chunk =
+// hbm_bytes / blocks rounded down to a power of two >= 8 KiB (used only when loads == 2); loads 0,
+// 1 or 2; mfmas a multiple of 8 up to 4096, not 0 when loads is 0; vary 0 or 1; clk holds 2 int64
+// per workgroup. 512 threads per workgroup.
+int vxf_mfma_mix(const void* l2, int64_t l2_bytes, const void* hbm, int64_t hbm_bytes, int loads, int mfmas, int vary,
+                 int blocks, int rounds, int* sink, int64_t* clk, void* stream) {
+  if (!l2 || !sink || !clk || blocks <= 0 || rounds <= 0) return 1;
+  if (l2_bytes < 16384 || (l2_bytes & (l2_bytes - 1)) != 0) return 1;
+  if (loads < 0 || loads > 2 || mfmas < 0 || mfmas % 8 != 0 || mfmas > 4096 || (!loads && mfmas == 0)) return 1;
+  if (vary != 0 && vary != 1) return 1;
+  int64_t chunk = 0;
+  if (loads == 2) {
+    if (!hbm || hbm_bytes / blocks < 8192) return 1;
+    chunk = 8192;
+    while (chunk * 2 <= hbm_bytes / blocks) chunk *= 2;
+  }
+  hipLaunchKernelGGL(mfma_mix_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, (const v4i*)l2,
+                     l2_bytes / 16 - 1, (const v4i*)hbm, chunk ? chunk / 16 - 1 : 0, loads, mfmas, vary, rounds, sink,
+                     clk);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
