@@ -99,6 +99,7 @@ class DecodeStep:
             caches.append((kv, kc, vc))
         bt = torch.randperm(B * nbp, device=self.dev, generator=gen).view(B, nbp).to(torch.int32)
         sl = torch.full((B,), L, device=self.dev, dtype=torch.int32)
+        self.max_seq_len = L  # the host bound vLLM's metadata passes with the step
         return caches, bt, sl
 
     def step(self, h, caches, bt, sl, exact=True):
@@ -120,7 +121,7 @@ class DecodeStep:
                 a += 1
                 o = torch.empty(B, ATT_H, ATT_D, device=h.device, dtype=torch.bfloat16)
                 self.P.paged_decode(qkv[:, :HIDDEN].view(B, ATT_H, ATT_D), kc, vc, bt, sl, ATT_D ** -0.5, o, B,
-                                    self.P.MAX_LEN)
+                                    self.max_seq_len)
                 mix = o.view(B, HIDDEN)
             else:
                 mix = qkv[:, :HIDDEN]
@@ -149,7 +150,7 @@ class DecodeStep:
 
         def attention(exact):
             for _, kc, vc in caches:
-                self.P.paged_decode(q, kc, vc, bt, sl, ATT_D ** -0.5, o, B, self.P.MAX_LEN)
+                self.P.paged_decode(q, kc, vc, bt, sl, ATT_D ** -0.5, o, B, self.max_seq_len)
 
         def rownorm(t):
             e = torch.frexp(t.abs().amax(dim=-1, keepdim=True).float()).exponent

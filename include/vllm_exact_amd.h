@@ -164,6 +164,13 @@ int vxa_paged_decode_workspace(int64_t n, int64_t num_heads, int64_t head_dim, i
  *   out      [>=n, H, D] strides (sot, soh), dtype VXA_F32 / VXA_BF16 / VXA_F16
  *   n        number of leading requests to compute (paged_attn.py:99)
  *   max_len  model maximum length: fixes NS = cdiv(max_len, split) (paged_attn.py:105)
+ *   max_seq_len  a bound on seq_lens[:n] (the reference's max_seq_len argument,
+ *            paged_attn.py:97, which it leaves unused), or 0 for none. The grid then covers
+ *            min(NS, cdiv(max_seq_len, split)) segments per request: every request within the
+ *            bound gets the bits of the full grid; a request longer than the bound (and within
+ *            max_len) gets NaN rows. The workspace needs the partials of that many segments
+ *            (vxa_paged_decode_workspace with max_len = min(max_len, max_seq_len)).
+ *            VXA_ERR_ARG when negative.
  *   split    keys per segment; blk keys per online-softmax step (16, 32 or 64);
  *            waves per workgroup (4 or 8). split, blk and waves fix the floating-point
  *            order; the result never depends on n or on the other requests.
@@ -174,8 +181,8 @@ int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh,
                      const int32_t* block_table, int64_t sbt, const int32_t* seq_lens,
                      float scale, void* out, int out_dtype, int64_t sot, int64_t soh,
                      int64_t n, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                     int64_t block_size, int64_t max_len, int64_t split, int64_t blk,
-                     int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream);
+                     int64_t block_size, int64_t max_len, int64_t max_seq_len, int64_t split,
+                     int64_t blk, int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream);
 
 /*
  * vxa_paged_decode for the first *n_live requests, with the count read on the device:
@@ -192,8 +199,8 @@ int vxa_paged_decode_prefix(const void* q, int64_t sqt, int64_t sqh,
                             float scale, void* out, int out_dtype, int64_t sot, int64_t soh,
                             int64_t n, const int32_t* n_live, int64_t num_heads,
                             int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-                            int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws,
-                            size_t ws_bytes, vxa_stream_t stream);
+                            int64_t max_len, int64_t max_seq_len, int64_t split, int64_t blk,
+                            int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream);
 
 /* Bytes of device memory vxa_exact_linear_op_noalloc holds per GPU (a file-scope array). */
 #define VXA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)

@@ -96,7 +96,8 @@ def test_entry_points_validate_before_launching():
     # paged decode: unsupported head size / group / split are reported as unsupported
     args = dict(q=fake, sqt=4096, sqh=128, kc=fake, skb=4096, skp=2048, skh=256, vc=fake, svb=4096, svp=2048,
                 svh=256, bt=fake, sbt=8, sl=fake, scale=0.1, out=fake, od=nx.VXA_BF16, sot=4096, soh=128, n=2,
-                H=32, KV=8, D=128, BS=16, max_len=1024, split=1024, blk=64, waves=4, ws=None, wsb=0, st=None)
+                H=32, KV=8, D=128, BS=16, max_len=1024, max_seq_len=0, split=1024, blk=64, waves=4, ws=None, wsb=0,
+                st=None)
 
     def call(**over):
         a = dict(args, **over)
@@ -109,6 +110,10 @@ def test_entry_points_validate_before_launching():
     assert call(split=131072) == nx.VXA_ERR_UNSUPPORTED  # a segment's block-table entries must fit in LDS
     assert call(H=30, KV=8) == nx.VXA_ERR_ARG
     assert call(max_len=4096) == nx.VXA_ERR_WORKSPACE
+    # a bound on the batch's lengths trims the grid to the segments it reaches (here two, whose
+    # partials need a workspace); a negative bound is refused
+    assert call(max_len=4096, max_seq_len=3000) == nx.VXA_ERR_WORKSPACE
+    assert call(max_seq_len=-1) == nx.VXA_ERR_ARG
     assert call(n=0) == nx.VXA_OK
 
     # the device-count variant: the same checks, and the count pointer is required

@@ -78,6 +78,40 @@ def test_device_count_limits_the_requests(L):
         P.paged_decode(q, kc, vc, bt, sl, scale, out, B, 0, n_live=torch.tensor([1], device=DEV))
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_length_bound_trims_the_grid_without_changing_bits(out_dtype):
+    """max_seq_len as a bound on the batch's lengths (0: none, the grid of MAX_LEN): the grid
+    then covers only the segments the bound reaches, 3 of the 8 at 5000 keys and 1 at 2048 (no
+    merge launch). Requests within the bound keep the full grid's bits, single- and
+    multi-segment alike; a request longer than the bound gets NaN rows and leaves the others
+    unchanged. The same through the device-count entry point."""
+    B, H, KV, D = 6, 8, 2, 128
+    q, kv, bt, sl = make_paged(B, 9000, 16, H, KV, D, seed=31)
+    sl = torch.tensor([100, 2048, 2049, 4096, 5000, 9000], dtype=torch.int32)
+    q, kv, bt, sl = (t.to(DEV) for t in (q, kv, bt, sl))
+    kc, vc = kv_views(kv, D)
+    scale = D ** -0.5
+    assert P.MAX_LEN == 16384 and P.SPLIT == 2048
+
+    def run(bound, n_live=None):
+        out = torch.full((B, H, D), float("nan"), device=DEV, dtype=out_dtype)
+        P.paged_decode(q, kc, vc, bt, sl, scale, out, B, bound, n_live=n_live)
+        return out.view(torch.int32 if out_dtype == torch.float32 else torch.int16)
+
+    full = run(0)
+    assert not torch.isnan(full.view(out_dtype)).any()
+    assert torch.equal(run(9000), full)
+    assert torch.equal(run(16384), full)
+    for bound, within in ((5000, 5), (2048, 2)):
+        for n_live in (None, torch.tensor([B], dtype=torch.int32, device=DEV)):
+            got = run(bound, n_live)
+            assert torch.equal(got[:within], full[:within]), (bound, n_live)
+            assert torch.isnan(got[within:].view(out_dtype)).all(), (bound, n_live)
+    want = _oracle(q, kv, bt, sl, scale, 5, D)
+    got = run(5000)[:5].view(out_dtype).float().cpu().numpy()
+    (_check_tol if out_dtype == torch.float32 else _check_tol_bf16)(got, want)
+
+
 @pytest.mark.parametrize("B,L,BS", [(8, 300, 16), (8, 5000, 528), (4, 9000, 528), (64, 8192, 528), (8, 3000, 8),
                                     (6, 2000, 24)])
 def test_paged_attention_reference_cases(B, L, BS):

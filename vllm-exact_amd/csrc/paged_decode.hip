@@ -24,6 +24,8 @@
 // Arithmetic is compiled with -ffp-contract=off; every fused multiply-add is written
 // explicitly, so the order is the one in the source.
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -40,7 +42,8 @@ struct PagedParams {
   const int32_t* sl;
   float scale_log2;  // softmax scale * log2(e)
   int32_t split;     // keys per segment (multiple of 16)
-  int32_t ns;        // segments per request in the grid
+  int32_t ns;        // segments per request in the grid (the caller's length bound may trim it)
+  int32_t ns_model;  // segments the model's maximum length fixes: NS = cdiv(max_len, split)
   int32_t H, KV;
   int32_t bs;        // page size (tokens per block)
   int32_t bs_shift;  // log2(bs) when bs is a power of two, else -1
@@ -120,6 +123,18 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
   if (p.n_live != nullptr && b >= *p.n_live) return;  // not a live request: nothing read or written
 
   const int L = p.sl[b];
+  // Segments the request needs, capped at the model's NS as the fixed grid caps them. A grid
+  // trimmed by the caller's bound on the batch's lengths covers every request within that
+  // bound with the same segments (the same bits); a longer request gets NaN rows, written by
+  // its segment-0 workgroups, instead of a sum over fewer keys.
+  const int need = min((L + p.split - 1) / p.split, p.ns_model);
+  if (need > p.ns) {
+    if (s == 0)
+      for (int idx = threadIdx.x; idx < G * D; idx += 64 * NW)
+        store_f32_as(p.out, p.out_dtype, (int64_t)b * p.sot + (int64_t)(g * G + idx / D) * p.soh + idx % D,
+                     __builtin_nanf(""));
+    return;
+  }
   const int start = s * p.split;
   if (start >= L) return;  // segment past the end: contributes exactly 0, never read
   const int end = min(start + p.split, L);
@@ -268,7 +283,7 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
   // Fixed-order merge of the waves, then either the final output (single-segment request)
   // or the segment partial.
   const int H = p.H;
-  const int nsb = min((L + p.split - 1) / p.split, p.ns);
+  const int nsb = need;
   for (int idx = threadIdx.x; idx < G * D; idx += 64 * NW) {
     const int h = idx / D, d = idx % D;
     float m = kNegInf, l = 0.0f, a = 0.0f;
@@ -299,8 +314,8 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
   const int head = (int)(bh % p.H);
   if (p.n_live != nullptr && b >= *p.n_live) return;
   const int L = p.sl[b];
-  const int nsb = min((L + p.split - 1) / p.split, p.ns);
-  if (nsb == 1) return;  // written by the partial kernel
+  const int nsb = min((L + p.split - 1) / p.split, p.ns_model);
+  if (nsb == 1 || nsb > p.ns) return;  // written by the partial kernel (NaN rows past a trimmed grid)
   const int lane = threadIdx.x;
   float m[DPW], l[DPW], a[DPW];
 #pragma unroll
@@ -385,9 +400,10 @@ int paged_decode_impl(const void* q, int64_t sqt, int64_t sqh, const void* k_cac
                       const int32_t* block_table, int64_t sbt, const int32_t* seq_lens, float scale, void* out,
                       int out_dtype, int64_t sot, int64_t soh, int64_t n, const int32_t* n_live,
                       int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-                      int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws, size_t ws_bytes,
-                      vxa_stream_t stream) {
-  if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || split <= 0)
+                      int64_t max_len, int64_t max_seq_len, int64_t split, int64_t blk, int64_t waves, void* ws,
+                      size_t ws_bytes, vxa_stream_t stream) {
+  if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || split <= 0 ||
+      max_seq_len < 0)
     return VXA_ERR_ARG;
   if (out_dtype != VXA_F32 && out_dtype != VXA_BF16 && out_dtype != VXA_F16) return VXA_ERR_ARG;
   if (num_heads % num_kv_heads != 0) return VXA_ERR_ARG;
@@ -406,9 +422,12 @@ int paged_decode_impl(const void* q, int64_t sqt, int64_t sqh, const void* k_cac
       skb % 8 || skp % 8 || skh % 8 || svb % 8 || svp % 8 || svh % 8)
     return VXA_ERR_UNSUPPORTED;
 
-  const int64_t ns = num_segments(max_len, split);
+  // The grid: the model's NS segments per request, or fewer when the caller bounds the batch's
+  // lengths (max_seq_len > 0); the workspace holds the partials of the grid's segments.
+  const int64_t ns_model = num_segments(max_len, split);
+  const int64_t ns = max_seq_len > 0 ? std::min(ns_model, num_segments(max_seq_len, split)) : ns_model;
   size_t need = 0;
-  vxa_paged_decode_workspace(n, num_heads, head_dim, max_len, split, &need);
+  vxa_paged_decode_workspace(n, num_heads, head_dim, ns * split, split, &need);
   if (need > 0 && (!ws || ws_bytes < need)) return VXA_ERR_WORKSPACE;
 
   PagedParams pp;
@@ -422,6 +441,7 @@ int paged_decode_impl(const void* q, int64_t sqt, int64_t sqh, const void* k_cac
   pp.scale_log2 = (float)((double)scale * 1.4426950408889634);
   pp.split = (int32_t)split;
   pp.ns = (int32_t)ns;
+  pp.ns_model = (int32_t)ns_model;
   pp.H = (int32_t)num_heads;
   pp.KV = (int32_t)num_kv_heads;
   pp.bs = (int32_t)block_size;
@@ -471,11 +491,11 @@ extern "C" int vxa_paged_decode(const void* q, int64_t sqt, int64_t sqh, const v
                                 int64_t svh, const int32_t* block_table, int64_t sbt, const int32_t* seq_lens,
                                 float scale, void* out, int out_dtype, int64_t sot, int64_t soh, int64_t n,
                                 int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-                                int64_t max_len, int64_t split, int64_t blk, int64_t waves, void* ws,
-                                size_t ws_bytes, vxa_stream_t stream) {
+                                int64_t max_len, int64_t max_seq_len, int64_t split, int64_t blk, int64_t waves,
+                                void* ws, size_t ws_bytes, vxa_stream_t stream) {
   return paged_decode_impl(q, sqt, sqh, k_cache, skb, skp, skh, v_cache, svb, svp, svh, block_table, sbt, seq_lens,
                            scale, out, out_dtype, sot, soh, n, nullptr, num_heads, num_kv_heads, head_dim,
-                           block_size, max_len, split, blk, waves, ws, ws_bytes, stream);
+                           block_size, max_len, max_seq_len, split, blk, waves, ws, ws_bytes, stream);
 }
 
 extern "C" int vxa_paged_decode_prefix(const void* q, int64_t sqt, int64_t sqh, const void* k_cache, int64_t skb,
@@ -484,10 +504,11 @@ extern "C" int vxa_paged_decode_prefix(const void* q, int64_t sqt, int64_t sqh, 
                                        const int32_t* seq_lens, float scale, void* out, int out_dtype,
                                        int64_t sot, int64_t soh, int64_t n, const int32_t* n_live,
                                        int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                                       int64_t block_size, int64_t max_len, int64_t split, int64_t blk,
-                                       int64_t waves, void* ws, size_t ws_bytes, vxa_stream_t stream) {
+                                       int64_t block_size, int64_t max_len, int64_t max_seq_len, int64_t split,
+                                       int64_t blk, int64_t waves, void* ws, size_t ws_bytes,
+                                       vxa_stream_t stream) {
   if (n_live == nullptr) return VXA_ERR_ARG;
   return paged_decode_impl(q, sqt, sqh, k_cache, skb, skp, skh, v_cache, svb, svp, svh, block_table, sbt, seq_lens,
                            scale, out, out_dtype, sot, soh, n, n_live, num_heads, num_kv_heads, head_dim,
-                           block_size, max_len, split, blk, waves, ws, ws_bytes, stream);
+                           block_size, max_len, max_seq_len, split, blk, waves, ws, ws_bytes, stream);
 }

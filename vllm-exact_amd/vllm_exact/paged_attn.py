@@ -35,14 +35,21 @@ def paged_decode(query, key_cache, value_cache, block_table, seq_lens, scale, ou
                  warps=None, stages=None, split=None, n_live=None):
     """query (>=n, H, D) bf16; key/value_cache (num_blocks, block_size, KV, D) bf16 views;
     block_table (B, max_blocks) int32; seq_lens (B,) int32; out (>=n, H, D).
-    Computes the first n requests only (paged_attn.py:97-114). max_seq_len is accepted and
-    unused, as in the reference: the grid is fixed by MAX_LEN.
+    Computes the first n requests only (paged_attn.py:97-114). The segments of SPLIT keys, and
+    so the bits of every request, are fixed by MAX_LEN as in the reference. max_seq_len, which
+    the reference accepts and leaves unused, is taken as a bound on seq_lens[:n] (vLLM's
+    metadata keeps it one, also under graph capture): the grid then covers only the segments
+    the bound can reach, which changes no bit of a request within it, and a request longer
+    than the bound gets NaN rows rather than a sum over fewer keys. 0 or None: no bound.
 
     n_live: optional int32 GPU tensor of one element holding a count <= n. Only the first
     n_live requests are then computed and written, the count read by the kernel itself, so a
     count produced on the GPU needs no host round trip (n still sizes the grid)."""
-    del max_seq_len, stages
+    del stages
     n = int(n)
+    bound = int(max_seq_len or 0)
+    if bound < 0:
+        raise ValueError(f"paged_decode: max_seq_len must be >= 0, got {bound}")
     if n <= 0:
         return out
     blk, warps, split = int(blk or BLK), int(warps or WARPS), int(split or SPLIT)
@@ -69,7 +76,7 @@ def paged_decode(query, key_cache, value_cache, block_table, seq_lens, scale, ou
     if n_live is not None and (not n_live.is_cuda or n_live.dtype != torch.int32 or n_live.numel() != 1
                                or n_live.device != query.device):
         raise ValueError("paged_decode: n_live must be a one-element int32 tensor on the query's GPU")
-    ws_bytes = _nx.paged_workspace(n, H, D, MAX_LEN, split)
+    ws_bytes = _nx.paged_workspace(n, H, D, min(MAX_LEN, bound) if bound else MAX_LEN, split)
     ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=query.device) if ws_bytes else None
     dev = query.device
     with torch.cuda.device(dev):
@@ -79,7 +86,7 @@ def paged_decode(query, key_cache, value_cache, block_table, seq_lens, scale, ou
                 value_cache.data_ptr(), value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
                 block_table.data_ptr(), block_table.stride(0), seq_lens.data_ptr(), float(scale),
                 out.data_ptr(), _nx.dtype_enum(out.dtype), out.stride(0), out.stride(1), n)
-        tail = (H, KV, D, BS, int(MAX_LEN), split, blk, warps, _nx.ptr(ws), ws_bytes, st)
+        tail = (H, KV, D, BS, int(MAX_LEN), bound, split, blk, warps, _nx.ptr(ws), ws_bytes, st)
         if n_live is None:
             _nx.check(_nx.lib().vxa_paged_decode(*head, *tail), "paged_decode")
         else:
