@@ -298,8 +298,10 @@ def _shipped_entries(path):
         kd = int(nk.split(",")[1])
         marks = set(row.get("one_launch", ()))
         for m, cfg in row.items():
-            if m != "one_launch":
+            if m not in ("one_launch", "n_split"):
                 out.add((int(m), kd, tuple(cfg), int(m) in marks))
+        for m, split in row.get("n_split", {}).items():  # the second launch of a column split
+            out.add((int(m), kd, tuple(split[1:]), False))
     return sorted(out)
 
 

@@ -71,6 +71,27 @@ def test_lm_head_full_width_through_the_op(monkeypatch, lm_weight, F):
         assert np.array_equal(got, want), (F, M, plugin._cfg(M, VOCAB, HIDDEN), int((got != want).sum()))
 
 
+def test_lm_head_column_split_gives_the_one_launch_bits(monkeypatch, lm_weight):
+    """The F = 14 table splits the lm_head's columns at 193-256 rows (the whole rounds of
+    workgroups, then the rest with a grid of its own): the op's output equals, bit for bit over
+    the whole width, one GEMM launch over all columns with the row's cfg."""
+    w, _ = lm_weight
+    F = 14
+    use(monkeypatch, F)
+    wbuf = plugin.pack_weight(w)
+    g = torch.Generator().manual_seed(30 + F)
+    for M in (256, 200):
+        split = plugin._n_split(M, VOCAB, HIDDEN)
+        assert split is not None and 0 < split[0] < VOCAB, (F, M)
+        x = torch.randn(M, HIDDEN, generator=g).to(torch.bfloat16).to(DEV)
+        y = torch.ops.exactmm.linear(x, *wbuf)
+        whole = torch.empty(M, VOCAB, device=DEV, dtype=torch.bfloat16)
+        K.exact_linear_packed(K.digitize_packed(x, F), (wbuf[0], wbuf[2], wbuf[3]), HIDDEN, F, F == 14, out=whole,
+                              cfg=plugin._cfg(M, VOCAB, HIDDEN))
+        assert torch.equal(y.view(torch.int16), whole.view(torch.int16)), (F, M, split)
+    assert all(plugin._n_split(m, VOCAB, HIDDEN) is None for m in (16, 192, 512))
+
+
 @pytest.mark.parametrize("N,Kd", SWEEP)
 def test_f15_table_through_the_op_at_sweep_shapes(monkeypatch, N, Kd):
     use(monkeypatch, 15)

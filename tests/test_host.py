@@ -73,6 +73,10 @@ def test_tuner_merge_keeps_untuned_entries():
     # a retune without marks (plain layout) leaves the base's marks alone
     assert tune.merge_row(got, {"256": a}, [256])["one_launch"] == [4, 16]
     assert tune.merge_row({}, {"64": c, "one_launch": []}, [64]) == {"64": c, "one_launch": []}
+    # a column split stays with its row until that row is retuned
+    split = {"256": [768] + a}
+    assert tune.merge_row({"256": c, "n_split": split}, {"16": a}, [16])["n_split"] == split
+    assert "n_split" not in tune.merge_row({"256": c, "n_split": split}, {"256": a}, [256])
 
 
 @pytest.mark.parametrize("path", [vllm_exact.TABLES["mi355x"], vllm_exact.TABLES_F15["mi355x"]])
@@ -85,6 +89,10 @@ def test_shipped_table_is_well_formed(path):
             if m == "one_launch":
                 assert all(str(r) in row for r in cfg), (nk, cfg)  # marks name tuned rows
                 continue
+            if m == "n_split":
+                for r, split in cfg.items():  # splits name tuned rows, at a tile boundary inside N
+                    assert r in row and 0 < split[0] < n and split[0] % 16 == 0 and 7 <= len(split[1:]) <= 8
+                continue
             assert int(m) > 0 and 7 <= len(cfg) <= 8
     plugin.load_table(path)
     plugin.load_table(None)
@@ -92,9 +100,39 @@ def test_shipped_table_is_well_formed(path):
     # other families through the plan's nearest-instantiation rule
     xw = {(bm, bn, r, nw) for bm, bn, r, nw in K.XW_SHAPES}
     for row in raw.values():
-        for m, cfg in row.items():
-            if m != "one_launch" and cfg[2] == 64:
+        cfgs = [c for m, c in row.items() if m not in ("one_launch", "n_split")]
+        cfgs += [split[1:] for split in row.get("n_split", {}).values()]
+        for cfg in cfgs:
+            if cfg[2] == 64:
                 assert (cfg[0], cfg[1], cfg[4], cfg[3]) in xw, cfg
+
+
+def test_column_split_lookup(tmp_path):
+    """A row's "n_split" entry applies to the calls whose row count _cfg maps to that tuned
+    row, and to no other; malformed entries are refused when the table loads."""
+    a, b = [128, 192, 128, 8, 2, 8, 1], [64, 96, 256, 8, 2, 8, 1]
+    t = {"1000,4096": {"64": a, "256": a, "n_split": {"256": [768] + b}}}
+    p = tmp_path / "t.json"
+    p.write_text(json.dumps(t))
+    try:
+        plugin.load_table(p)
+        assert plugin._n_split(256, 1000, 4096) == (768, tuple(b))
+        assert plugin._n_split(65, 1000, 4096) == (768, tuple(b))  # M 65 .. 256 take the 256 row
+        assert plugin._n_split(64, 1000, 4096) is None
+        assert plugin._n_split(257, 1000, 4096) is None  # past the table: the last row, unsplit
+        assert plugin._n_split(256, 2000, 4096) is None
+        assert plugin._cfg(256, 1000, 4096) == tuple(a)
+        for bad in ([770] + b, [1000] + b, [768, 64, 96]):
+            t["1000,4096"]["n_split"] = {"256": bad}
+            p.write_text(json.dumps(t))
+            with pytest.raises(ValueError, match="n_split"):
+                plugin.load_table(p)
+        t["1000,4096"]["n_split"] = {"128": [768] + b}  # names no tuned row
+        p.write_text(json.dumps(t))
+        with pytest.raises(ValueError, match="n_split"):
+            plugin.load_table(p)
+    finally:
+        plugin.load_table(None)
 
 
 def test_bench_traffic_is_tied_to_cfg_and_sources(tmp_path, monkeypatch):

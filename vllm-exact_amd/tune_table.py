@@ -156,8 +156,8 @@ def merge_row(old, new, ms):
     """Row `old` with the tuned entries of `new` (at the row counts `ms`) put in. A row without
     a "one_launch" list follows the op's default (1-4 rows); merged, it keeps that meaning for
     the entries that were not retuned."""
-    cfgs = {m: c for m, c in old.items() if m != "one_launch"}
-    cfgs.update({m: c for m, c in new.items() if m != "one_launch"})
+    cfgs = {m: c for m, c in old.items() if m not in ("one_launch", "n_split")}
+    cfgs.update({m: c for m, c in new.items() if m not in ("one_launch", "n_split")})
     out = dict(sorted(cfgs.items(), key=lambda t: int(t[0])))
     if "one_launch" in new:
         if "one_launch" in old:
@@ -167,6 +167,10 @@ def merge_row(old, new, ms):
         out["one_launch"] = sorted(set(kept) | set(new["one_launch"]))
     elif "one_launch" in old:
         out["one_launch"] = old["one_launch"]
+    # column splits are measured against their row's cfg: a retuned row drops its split
+    split = {m: v for m, v in old.get("n_split", {}).items() if int(m) not in ms}
+    if split:
+        out["n_split"] = split
     return out
 
 

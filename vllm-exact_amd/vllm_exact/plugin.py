@@ -23,15 +23,19 @@ WEIGHT_RB = 32768  # weight rows digitized per block at load time (plugin.py:74)
 
 
 _ONE_LAUNCH_ROWS = {}  # (N, K) -> tuned row counts whose calls digitize inside the GEMM launch
+_N_SPLIT = {}  # (N, K) -> {tuned row count: (N1, cfg of columns N1..N)}
 
 
 def load_table(path):
     """Tuning table {"N,K": {"M": [BM, BN, BK, warps, stages, GM, SK(, mma)]}} (plugin.py:27-34).
     Configs change speed only, never results. A row may also hold "one_launch": [M, ...], the
-    tuned row counts at which the op digitizes inside the GEMM launch (see _one_launch)."""
+    tuned row counts at which the op digitizes inside the GEMM launch (see _one_launch), and
+    "n_split": {"M": [N1, BM, BN, ...]}, the tuned row counts at which the GEMM runs as two
+    launches over columns [0, N1) and [N1, N), the second with its own cfg (see _n_split)."""
     global _TABLE
     _ONE_LAUNCH_ROWS.clear()
     _ONE_LAUNCH_CFG.clear()
+    _N_SPLIT.clear()
     if path is None:
         _TABLE = None
         return
@@ -39,9 +43,17 @@ def load_table(path):
     _TABLE = {}
     for nk, row in raw.items():
         key = tuple(int(v) for v in nk.split(","))
-        _TABLE[key] = {int(m): tuple(c) for m, c in row.items() if m != "one_launch"}
+        _TABLE[key] = {int(m): tuple(c) for m, c in row.items() if m not in ("one_launch", "n_split")}
         if "one_launch" in row:
             _ONE_LAUNCH_ROWS[key] = frozenset(int(m) for m in row["one_launch"])
+        if "n_split" in row:
+            split = {}
+            for m, v in row["n_split"].items():
+                n1, cfg2 = int(v[0]), tuple(v[1:])
+                if int(m) not in _TABLE[key] or n1 <= 0 or n1 % 16 or n1 >= key[0] or len(cfg2) < 6:
+                    raise ValueError(f"load_table: bad n_split entry {m}: {v} for shape {nk}")
+                split[int(m)] = (n1, cfg2)
+            _N_SPLIT[key] = split
 
 
 # Built-in gfx950 configs when a shape has no table entry (speed only).
@@ -74,6 +86,20 @@ def _one_launch(M, N, Kd):
             return False
         return next(m for m in ms if m >= M) in _ONE_LAUNCH_ROWS[(N, Kd)]
     return M <= K.ONE_LAUNCH_MAX_ROWS
+
+
+def _n_split(M, N, Kd):
+    """(N1, cfg2) when the table row that _cfg picks for an (M, N, K) call splits its columns:
+    the GEMM then runs over columns [0, N1) with _cfg's config and over [N1, N) with cfg2, on the
+    same digits of x. N1 ends the last whole round of workgroups of the first config (one per CU),
+    so the last, partly filled round runs with a grid of its own. Integer sums do not depend on
+    the tiling: the bits are those of one launch. None otherwise."""
+    if _TABLE is None or (N, Kd) not in _N_SPLIT:
+        return None
+    ms = sorted(_TABLE[(N, Kd)])
+    if M > ms[-1]:
+        return None
+    return _N_SPLIT[(N, Kd)].get(next(m for m in ms if m >= M))
 
 
 # (F, trunc, cfg, N, K[, M at F = 15]) the one-launch digitize + GEMM path refused. At F < 15
@@ -119,7 +145,16 @@ def exact_linear_op(x: torch.Tensor, wh: torch.Tensor, wl: torch.Tensor, cw: tor
                 except NotImplementedError:
                     if K.bf16x_rows_aligned(xb):
                         _ONE_LAUNCH_CFG[key] = False  # refused for the cfg (and shape), not for this x
-            K.exact_linear_packed(K.digitize_packed(xb, F), (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
+            xd = K.digitize_packed(xb, F)
+            split = _n_split(xb.shape[0], N, Kd)
+            if split is None:
+                K.exact_linear_packed(xd, (wh, cw, sw), Kd, F, TRUNC, out=out[i:i + RB], cfg=cfg)
+            else:
+                # the whole rounds of workgroups, then the rest of the columns with a grid of its own
+                n1, cfg2 = split
+                ob = out[i:i + RB]
+                K.exact_linear_packed(xd, (wh[:n1 // 16], cw[:n1], sw[:n1]), Kd, F, TRUNC, out=ob[:, :n1], cfg=cfg)
+                K.exact_linear_packed(xd, (wh[n1 // 16:], cw[n1:], sw[n1:]), Kd, F, TRUNC, out=ob[:, n1:], cfg=cfg2)
         else:
             K.exact_linear(K.digitize(xb, F), (wh, wl, cw, sw), F, TRUNC, out=out[i:i + RB], cfg=cfg)
     return out.reshape(*shp[:-1], N)
