@@ -16,7 +16,9 @@ Up to 64 rows on packed weights, every cfg the one-launch digitize + GEMM
 kernel takes is also timed on that path; it is chosen, and M listed in the row's
 "one_launch", when it beats digitize + the best two-launch GEMM timed together. The result
 is {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK], "one_launch": [M, ...]}}; with
---merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept. OUT
+--merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept (a
+row's "n_split" column splits, which the op reads but this tuner does not search, stay with
+the rows that were not retuned). OUT
 is rewritten after every shape. The report also records the bf16 hipBLASLt time of the same product (torch.matmul) for
 comparison.
 """
