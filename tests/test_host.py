@@ -77,6 +77,16 @@ def test_tuner_merge_keeps_untuned_entries():
     split = {"256": [768] + a}
     assert tune.merge_row({"256": c, "n_split": split}, {"16": a}, [16])["n_split"] == split
     assert "n_split" not in tune.merge_row({"256": c, "n_split": split}, {"256": a}, [256])
+    assert tune.merge_row({"256": c, "n_split": split}, {"256": a, "n_split": {"256": [512] + a}},
+                          [256])["n_split"] == {"256": [512] + a}
+    # the split the tuner searches: the last whole round of one-per-CU K-split workgroups
+    xk = (128, 192, 128, 8, 2, 8, 1)
+    assert tune.whole_round_columns(256, 151936, xk, 256) == 147456  # 1584 workgroups: 6 rounds + 48
+    assert tune.whole_round_columns(512, 151936, xk, 256) == 147456  # 3168: 12 rounds + 96
+    assert tune.whole_round_columns(128, 151936, (128, 128, 128, 8, 2, 8, 1), 256) is None  # last round 64 % full
+    assert tune.whole_round_columns(256, 24576, xk, 256) is None  # exactly one round
+    assert tune.whole_round_columns(256, 151936, (16, 64, 128, 4, 1, 8, 1), 256) is None  # not K-split
+    assert tune.whole_round_columns(256, 151936, xk[:6] + (2,), 256) is None  # split-K
 
 
 @pytest.mark.parametrize("path", [vllm_exact.TABLES["mi355x"], vllm_exact.TABLES_F15["mi355x"]])

@@ -16,9 +16,10 @@ Up to 64 rows on packed weights, every cfg the one-launch digitize + GEMM
 kernel takes is also timed on that path; it is chosen, and M listed in the row's
 "one_launch", when it beats digitize + the best two-launch GEMM timed together. The result
 is {"N,K": {"M": [BM, BN, BK, waves, stages, GM, SK], "one_launch": [M, ...]}}; with
---merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept (a
-row's "n_split" column splits, which the op reads but this tuner does not search, stay with
-the rows that were not retuned). OUT
+--merge the tuned (N, K, M) entries replace those of BASE and the rest of BASE is kept. Where
+the chosen K-split cfg's grid ends in a round of workgroups at most half full, the columns of
+the whole rounds plus the rest under a second cfg are timed as a pair, and kept as the row's
+"n_split": {M: [N1, cfg...]} when 1 % faster. OUT
 is rewritten after every shape. The report also records the bf16 hipBLASLt time of the same product (torch.matmul) for
 comparison.
 """
@@ -39,6 +40,22 @@ DEFAULT_SHAPES = ("6144x4096,151936x4096,10240x4096,4096x4096,12288x4096,64x4096
 SPLITS = (1, 2, 4)
 ONE_LAUNCH_TUNE_ROWS = 64  # the one-launch path is timed up to this many rows
 FINALISTS = 6  # candidates per path re-timed in full after the first cut
+SPLIT_GAIN = 1.01  # a column split is kept when it is this much faster than one launch
+
+
+def whole_round_columns(M, N, cfg, ncu):
+    """N1, the columns of the last whole round of workgroups when cfg runs the K-split family
+    (8 waves, one workgroup per CU) with SK = 1 and its grid ends in a round at most half full;
+    None otherwise."""
+    bm, bn, bk, waves, stages = cfg[:5]
+    if waves != 8 or stages != 2 or bk not in (128, 256) or bm < 64 or cfg[6] != 1:
+        return None
+    nbm, nbn = -(-M // bm), -(-N // bn)
+    rounds, rest = divmod(nbm * nbn, ncu)
+    if rounds == 0 or rest == 0 or rest > ncu // 2 or (rounds * ncu) % nbm:
+        return None
+    n1 = rounds * ncu // nbm * bn
+    return n1 if 0 < n1 < N else None
 
 
 def timing_for(M, N, Kd, rot):
@@ -75,7 +92,8 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
     else:
         wds = [K.digitize(w, F) for _ in range(rot)]
     wbs = [w.clone() for _ in range(rot)]  # bf16 copies for the hipBLASLt comparison
-    row, one_rows = {}, []
+    ncu = torch.cuda.get_device_properties(w.device).multi_processor_count
+    row, one_rows, splits = {}, [], {}
     for M in ms:
         x = torch.randn(M, Kd, device="cuda", generator=gen).to(torch.bfloat16)
         xd = K.digitize_packed(x, F) if packed else K.digitize(x, F)
@@ -140,6 +158,35 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
             if best_one[0] < t_two:
                 best = best_one
                 one_rows.append(M)
+        n1 = whole_round_columns(M, N, best[1], ncu) if packed and not rec.get("one_launch") else None
+        if n1 is not None:
+            # the whole rounds with the chosen cfg, the rest of the columns with a grid of its own
+            # (the remainder's candidates cut on the remainder alone, then timed as the pair)
+            out = torch.empty(M, N, device="cuda", dtype=torch.float32)
+
+            def part(i, n0, n_end, cfg, xd=xd, out=out):
+                pw, cw, sw = wds[i]
+                return K.exact_linear_packed(xd, (pw[n0 // 16:(n_end + 15) // 16], cw[n0:n_end], sw[n0:n_end]),
+                                             Kd, F, trunc, out=out[:, n0:n_end], cfg=cfg)
+
+            rest = []
+            for cfg in candidates(M, Kd):
+                if cfg[6] != 1:
+                    continue
+                try:
+                    part(0, n1, N, cfg)
+                except NotImplementedError:
+                    continue
+                rest.append((timed(lambda i, c=cfg: part(i, n1, N, c), quick=True), cfg))
+            pairs = []
+            for _, cfg2 in sorted(rest)[:3]:
+                part(0, 0, n1, best[1])
+                part(0, n1, N, cfg2)
+                check(out.clone(), (best[1], n1, cfg2))
+                pairs.append((timed(lambda i, c=cfg2: (part(i, 0, n1, best[1]), part(i, n1, N, c))), cfg2))
+            if pairs and min(pairs)[0] * SPLIT_GAIN < best[0]:
+                splits[str(M)] = [n1] + list(min(pairs)[1])
+                rec.update(n_split=splits[str(M)], split_us=round(min(pairs)[0], 2))
         t_bf16 = timed(lambda i: torch.matmul(x, wbs[i].T))
         row[str(M)] = list(best[1])
         rec.update(bf16_hipblaslt_us=round(t_bf16, 2), chosen=list(best[1]))
@@ -149,6 +196,8 @@ def tune_shape(N, Kd, ms, F, trunc, gen, report, packed):
         report.append(rec)
     if packed:
         row["one_launch"] = one_rows
+    if splits:
+        row["n_split"] = splits
     del wds, wbs
     torch.cuda.empty_cache()
     return row
@@ -169,8 +218,9 @@ def merge_row(old, new, ms):
         out["one_launch"] = sorted(set(kept) | set(new["one_launch"]))
     elif "one_launch" in old:
         out["one_launch"] = old["one_launch"]
-    # column splits are measured against their row's cfg: a retuned row drops its split
+    # column splits are measured against their row's cfg: a retuned row takes the new result
     split = {m: v for m, v in old.get("n_split", {}).items() if int(m) not in ms}
+    split.update(new.get("n_split", {}))
     if split:
         out["n_split"] = split
     return out
