@@ -308,7 +308,8 @@ __global__ __launch_bounds__(64 * NW) void paged_partial_kernel(PagedParams p) {
 // Fixed-order merge over the segments of one (request, head); one wave per (b, head).
 template <int D>
 __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
-  constexpr int DPW = (D + 63) / 64;
+  static_assert(D % 64 == 0, "a lane owns D / 64 columns");
+  constexpr int DPW = D / 64;
   const int64_t bh = blockIdx.x;
   const int b = (int)(bh / p.H);
   const int head = (int)(bh % p.H);
@@ -324,20 +325,32 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
     l[j] = 0.0f;
     a[j] = 0.0f;
   }
+  // Segments are merged in index order, kChunk of them per pass: a pass issues every load of its
+  // segments first (indices past the last segment are clamped to it, read and left unmerged),
+  // so a pass waits for one memory latency rather than one per segment.
+  constexpr int kChunk = 8;
   const int64_t base = bh * p.ns;
-  for (int s = 0; s < nsb; ++s) {
-    const float ms = p.mp[base + s];
-    const float ls = p.lp[base + s];
+  for (int s0 = 0; s0 < nsb; s0 += kChunk) {
+    float ms[kChunk], ls[kChunk], as_[kChunk][DPW];
 #pragma unroll
-    for (int j = 0; j < DPW; ++j) {
-      const int d = lane + 64 * j;
-      if (d < D) merge_state(m[j], l[j], a[j], ms, ls, p.ap[(base + s) * D + d]);
+    for (int c = 0; c < kChunk; ++c) {
+      const int64_t s = base + min(s0 + c, nsb - 1);
+      ms[c] = p.mp[s];
+      ls[c] = p.lp[s];
+#pragma unroll
+      for (int j = 0; j < DPW; ++j) as_[c][j] = p.ap[s * D + lane + 64 * j];
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (s0 + c >= nsb) break;
+#pragma unroll
+      for (int j = 0; j < DPW; ++j) merge_state(m[j], l[j], a[j], ms[c], ls[c], as_[c][j]);
     }
   }
 #pragma unroll
   for (int j = 0; j < DPW; ++j) {
     const int d = lane + 64 * j;
-    if (d < D) store_f32_as(p.out, p.out_dtype, (int64_t)b * p.sot + (int64_t)head * p.soh + d, a[j] / l[j]);
+    store_f32_as(p.out, p.out_dtype, (int64_t)b * p.sot + (int64_t)head * p.soh + d, a[j] / l[j]);
   }
 }
 
