@@ -313,11 +313,31 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
   const int64_t bh = blockIdx.x;
   const int b = (int)(bh / p.H);
   const int head = (int)(bh % p.H);
+  const int lane = threadIdx.x;
+  // Segments are merged in index order, kChunk of them per pass, and a pass issues every load of
+  // its segments first, so it waits for one memory latency rather than one per segment. The
+  // first pass's loads go out before the request's length is read: they take segments
+  // min(c, ns - 1), inside the workspace whatever the length; later passes clamp to the request's
+  // last segment. A segment at or past that count is read and never merged.
+  constexpr int kChunk = 8;
+  const int64_t base = bh * p.ns;
+  float ms[kChunk], ls[kChunk], as_[kChunk][DPW];
+  auto load_pass = [&](int s0, int last) {
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int64_t s = base + min(s0 + c, last);
+      ms[c] = p.mp[s];
+      ls[c] = p.lp[s];
+#pragma unroll
+      for (int j = 0; j < DPW; ++j) as_[c][j] = p.ap[s * D + lane + 64 * j];
+    }
+  };
+  load_pass(0, p.ns - 1);
+  asm volatile("" ::: "memory");  // the loads above stay above the reads of the length below
   if (p.n_live != nullptr && b >= *p.n_live) return;
   const int L = p.sl[b];
   const int nsb = min((L + p.split - 1) / p.split, p.ns_model);
   if (nsb == 1 || nsb > p.ns) return;  // written by the partial kernel (NaN rows past a trimmed grid)
-  const int lane = threadIdx.x;
   float m[DPW], l[DPW], a[DPW];
 #pragma unroll
   for (int j = 0; j < DPW; ++j) {
@@ -325,27 +345,16 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(PagedParams p) {
     l[j] = 0.0f;
     a[j] = 0.0f;
   }
-  // Segments are merged in index order, kChunk of them per pass: a pass issues every load of its
-  // segments first (indices past the last segment are clamped to it, read and left unmerged),
-  // so a pass waits for one memory latency rather than one per segment.
-  constexpr int kChunk = 8;
-  const int64_t base = bh * p.ns;
-  for (int s0 = 0; s0 < nsb; s0 += kChunk) {
-    float ms[kChunk], ls[kChunk], as_[kChunk][DPW];
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      const int64_t s = base + min(s0 + c, nsb - 1);
-      ms[c] = p.mp[s];
-      ls[c] = p.lp[s];
-#pragma unroll
-      for (int j = 0; j < DPW; ++j) as_[c][j] = p.ap[s * D + lane + 64 * j];
-    }
+  for (int s0 = 0;;) {
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
       if (s0 + c >= nsb) break;
 #pragma unroll
       for (int j = 0; j < DPW; ++j) merge_state(m[j], l[j], a[j], ms[c], ls[c], as_[c][j]);
     }
+    s0 += kChunk;
+    if (s0 >= nsb) break;
+    load_pass(s0, nsb - 1);
   }
 #pragma unroll
   for (int j = 0; j < DPW; ++j) {
