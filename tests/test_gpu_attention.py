@@ -211,6 +211,25 @@ def test_other_constant_sets_are_invariant_too(blk, waves, split):
     _check_tol(full[[0, 11]].cpu().numpy(), want)
 
 
+def test_merge_of_more_segments_than_one_pass_loads():
+    """The merge loads eight segments a pass: requests of 1, 2, 8, 9, 16, 17 and 18 segments of
+    512 keys (pass boundaries on both sides) against the float64 oracle, each request's bits the
+    same alone as in the batch, and the same with the batch's length passed as the bound (a grid
+    of 18 segments instead of 32) as with none."""
+    D, split = 128, 512
+    q, kv, bt, sl = _gpu_paged(7, 9216, seed=23, var_len=False)
+    sl = torch.tensor([512, 513, 4096, 4097, 8192, 8193, 9216], device=DEV, dtype=torch.int32)
+    kc, vc = kv_views(kv, D)
+    full = torch.full((7, 32, D), float("nan"), device=DEV)
+    P.paged_decode(q, kc, vc, bt, sl, 0.09, full, 7, 0, split=split)
+    bounded = _run(q, kv, bt, sl, 0.09, 7, D, split=split)
+    assert torch.equal(bounded, full)
+    for b in range(7):
+        alone = _run(q[b:b + 1], kv, bt[b:b + 1], sl[b:b + 1], 0.09, 1, D, split=split)
+        assert torch.equal(alone[0], full[b]), b
+    _check_tol(full.cpu().numpy(), _oracle(q, kv, bt, sl, 0.09, 7, D))
+
+
 @pytest.mark.parametrize("D,H,KV", [(64, 8, 8), (128, 16, 8), (256, 32, 4)])
 def test_head_dims_and_groups(D, H, KV):
     q, kv, bt, sl = make_paged(5, 700, 32, H, KV, D, seed=D + H)
