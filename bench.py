@@ -632,6 +632,7 @@ def floors(args):
     lib.vxf_l2.argtypes = [vp, i64, i32, i32, i32, i32, i32, vp, vp, vp]
     lib.vxf_lds.argtypes = [i32, i32, i32, vp, vp, vp]
     lib.vxf_mfma.argtypes = [i32, i32, i32, vp, vp, vp]
+    lib.vxf_mfma_shape.argtypes = [i32, i32, i32, i32, vp, vp, vp]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     ncu = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -680,6 +681,23 @@ def floors(args):
         log("mfma", mf[-1])
     out["mfma_i8_16x16x64"] = mf
     ghz = mf[0]["ghz"]
+
+    # The two INT8 MFMA shapes at equal work, 8 waves per CU: operands the same in every
+    # instruction, or random with a different set in every instruction (the power a GEMM's
+    # digit fragments draw sets the clock)
+    ms = []
+    for shape in (16, 32):
+        for rnd in (0, 1):
+            rounds = 8192
+            us, _, ghz_run = timed(lambda: check(lib.vxf_mfma_shape(shape, rnd, ncu, rounds, sink.data_ptr(),
+                                                                    cyc.data_ptr(), st())), ncu)
+            ops = ncu * 8 * rounds * 8 * 16 * 16 * 64 * 2
+            peak_per_ghz = ncu * 4 * 2048 * 1e9  # INT8 ops per second per GHz: 2048 per clock per SIMD
+            ms.append({"shape": f"{shape}x{shape}x{1024 // shape}", "operands": "random" if rnd else "constant",
+                       "us": round(us, 1), "ghz": round(ghz_run, 3), "TOPS": round(ops / us / 1e6, 1),
+                       "frac_of_peak_at_clock": round(ops / (us * 1e-6) / (peak_per_ghz * ghz_run), 3)})
+            log("mfma_shape", ms[-1])
+    out["mfma_i8_shapes"] = ms
 
     # LDS reads: ds_read_b128, 8 in flight per lane
     ld = []

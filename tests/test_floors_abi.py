@@ -1,5 +1,5 @@
 """The probe library behind `bench.py --floors` (vllm-exact_amd/floors/floors.hip): it loads,
-exports its six probes, and refuses malformed arguments before launching anything (no GPU
+exports its eight probes, and refuses malformed arguments before launching anything (no GPU
 needed: every refusal happens on the host)."""
 import ctypes
 from pathlib import Path
@@ -18,6 +18,7 @@ SIGS = {
     "vxf_lds": [i32, i32, i32, vp, vp, vp],
     "vxf_mfma": [i32, i32, i32, vp, vp, vp],
     "vxf_mfma_mix": [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp],
+    "vxf_mfma_shape": [i32, i32, i32, i32, vp, vp, vp],
 }
 
 
@@ -62,3 +63,8 @@ def test_probes_refuse_malformed_arguments(lib):
     assert lib.vxf_mfma_mix(p, 1 << 21, None, 1 << 30, 2, 56, 0, 1, 1, p, p, None) == 1
     assert lib.vxf_mfma_mix(p, 1 << 21, p, 4096, 2, 56, 0, 1, 1, p, p, None) == 1
     assert lib.vxf_mfma_mix(p, 1 << 21, p, 1 << 30, 1, 56, 2, 1, 1, p, p, None) == 1
+    # mfma_shape: an unknown shape or operand mode, an odd round count, no clock buffer
+    assert lib.vxf_mfma_shape(24, 0, 1, 2, p, p, None) == 1
+    assert lib.vxf_mfma_shape(16, 2, 1, 2, p, p, None) == 1
+    assert lib.vxf_mfma_shape(32, 1, 1, 3, p, p, None) == 1
+    assert lib.vxf_mfma_shape(16, 1, 1, 2, p, None, None) == 1

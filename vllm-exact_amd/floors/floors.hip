@@ -12,6 +12,9 @@
 //            global_load_lds_dwordx4, at Q loads in flight per lane
 //   lds      ds_read_b128 of LDS into VGPRs
 //   mfma     v_mfma_i32_16x16x64_i8 on 8 independent accumulators per wave
+//   mfma_shape  the two INT8 MFMA shapes at equal work per round (16x16x64 on 8 accumulators,
+//            32x32x32 on 4), their operands the same in every instruction or drawn at random
+//            with a different set in every instruction (as a GEMM's digit fragments are)
 //   mfma_mix MFMAs and loads (L2-resident, or L2 and HBM) at once, in the large-M exact GEMM's
 //            proportion, with the shader clock each workgroup ran at
 //
@@ -25,6 +28,7 @@
 #include <stdint.h>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 namespace {
@@ -193,6 +197,65 @@ __global__ __launch_bounds__(1024) void mfma_kernel(int rounds, int* sink, int64
   finish(sink, cycles, acc, t0);
 }
 
+// 8 waves per workgroup. SHAPE 16: 8 v_mfma_i32_16x16x64_i8 a round on 8 accumulators;
+// SHAPE 32: 4 v_mfma_i32_32x32x32_i8 a round on 4 accumulators (the same integer work), rounds
+// taken in pairs. RANDOM: eight operand sets drawn from a per-lane linear congruential sequence
+// before the loop, instruction i of a round (or of a round pair, for SHAPE 32) using set i, so
+// consecutive instructions see different random bits and no operand is rewritten in the loop;
+// else every instruction takes the same operands.
+template <int SHAPE, bool RANDOM>
+__global__ __launch_bounds__(512) void mfma_shape_kernel(int rounds, int* sink, int64_t* cycles) {
+  const Stamp t0 = stamp();
+  v4i as[8], bs[8];
+  uint32_t x = threadIdx.x * 2654435761u + blockIdx.x * 40503u + 1u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (RANDOM || i == 0) {
+      uint32_t t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x = x * 1664525u + 1013904223u;
+        t[j] = x;
+      }
+      as[i] = v4i{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+      bs[i] = v4i{(int)t[4], (int)t[5], (int)t[6], (int)t[7]};
+    } else {
+      as[i] = as[0];
+      bs[i] = bs[0];
+    }
+  }
+  v4i acc = {0, 0, 0, 0};
+  if constexpr (SHAPE == 16) {
+    v4i c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = v4i{i, 0, 0, 0};
+    for (int r = 0; r < rounds; ++r) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[i], bs[i], c[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc ^= c[i];
+  } else {
+    v16i c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[i] = v16i{};
+      c[i][0] = i;
+    }
+    for (int r = 0; r < rounds; r += 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(as[i], bs[i], c[i], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(as[i + 4], bs[i + 4], c[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 16; j += 4) acc ^= v4i{c[i][j], c[i][j + 1], c[i][j + 2], c[i][j + 3]};
+  }
+  finish(sink, cycles, acc, t0);
+}
+
 // MFMAs and loads together, the mix of the large-M exact GEMM: 8 waves per workgroup, one
 // workgroup per CU. Each round a wave issues eight 16-byte loads per lane (8 KiB) when
 // loads > 0: all from the L2-resident buffer `l2` (offsets masked into it), or with loads == 2
@@ -341,6 +404,20 @@ int vxf_lds(int waves, int blocks, int rounds, int* sink, int64_t* cycles, void*
 int vxf_mfma(int waves, int blocks, int rounds, int* sink, int64_t* cycles, void* stream) {
   if (!sink || !cycles || blocks <= 0 || rounds <= 0 || (waves != 4 && waves != 8 && waves != 16)) return 1;
   hipLaunchKernelGGL(mfma_kernel, dim3(blocks), dim3(64 * waves), 0, (hipStream_t)stream, rounds, sink, cycles);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// mfma_shape: shape 16 or 32, random 0 or 1, rounds even and positive; 512 threads a workgroup.
+int vxf_mfma_shape(int shape, int random, int blocks, int rounds, int* sink, int64_t* cycles, void* stream) {
+  if (!sink || !cycles || blocks <= 0 || rounds <= 0 || rounds % 2 || (shape != 16 && shape != 32) ||
+      (random != 0 && random != 1))
+    return 1;
+  const hipStream_t st = (hipStream_t)stream;
+#define VXF_SHAPE(S, R)                                                                                     \
+  if (shape == S && random == R)                                                                            \
+    hipLaunchKernelGGL((mfma_shape_kernel<S, R != 0>), dim3(blocks), dim3(512), 0, st, rounds, sink, cycles);
+  VXF_SHAPE(16, 0) VXF_SHAPE(16, 1) VXF_SHAPE(32, 0) VXF_SHAPE(32, 1)
+#undef VXF_SHAPE
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
