@@ -808,6 +808,23 @@ def floors(args):
     out["stream_read"] = stream_rows
     out["empty_launch_us"] = round(empty_us, 2)
 
+    # The packed digitize (the op's first launch) against a copy with its grid and traffic and no
+    # arithmetic, graph replay with the launch included, inputs rotated over four copies
+    from vllm_exact import kernels as K
+    lib.vxf_rowcopy.argtypes = [vp, i64, i64, i64, vp, i64, vp]
+    dg = []
+    for rows, k in ((64, 4096), (256, 4096), (256, 12288)):
+        xs = [torch.randn(rows, k, device=dev).to(torch.bfloat16) for _ in range(4)]
+        hbuf = torch.empty(rows * k * 2, device=dev, dtype=torch.int8)
+        t_dig = statistics.median(time_graph(lambda i: K.digitize_packed(xs[i], 14), 4) for _ in range(3))
+        t_copy = statistics.median(
+            time_graph(lambda i: check(lib.vxf_rowcopy(xs[i].data_ptr(), xs[i].numel() * 2, rows, k, hbuf.data_ptr(),
+                                                       hbuf.numel(), st())), 4) for _ in range(3))
+        dg.append({"rows": rows, "K": k, "digitize_us": round(t_dig, 2), "rowcopy_us": round(t_copy, 2)})
+        log("digitize", dg[-1])
+        del xs, hbuf
+    out["digitize_vs_rowcopy"] = dg
+
     # Permuted 8 KiB pages (the paged KV stream): 1 GiB, each page read once
     nb = 1 << 30
     pbuf = torch.empty(nb, device=dev, dtype=torch.uint8)

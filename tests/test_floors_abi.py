@@ -1,5 +1,5 @@
 """The probe library behind `bench.py --floors` (vllm-exact_amd/floors/floors.hip): it loads,
-exports its eight probes, and refuses malformed arguments before launching anything (no GPU
+exports its nine probes, and refuses malformed arguments before launching anything (no GPU
 needed: every refusal happens on the host)."""
 import ctypes
 from pathlib import Path
@@ -19,6 +19,7 @@ SIGS = {
     "vxf_mfma": [i32, i32, i32, vp, vp, vp],
     "vxf_mfma_mix": [vp, i64, vp, i64, i32, i32, i32, i32, i32, vp, vp, vp],
     "vxf_mfma_shape": [i32, i32, i32, i32, vp, vp, vp],
+    "vxf_rowcopy": [vp, i64, i64, i64, vp, i64, vp],
 }
 
 
@@ -68,3 +69,9 @@ def test_probes_refuse_malformed_arguments(lib):
     assert lib.vxf_mfma_shape(16, 2, 1, 2, p, p, None) == 1
     assert lib.vxf_mfma_shape(32, 1, 1, 3, p, p, None) == 1
     assert lib.vxf_mfma_shape(16, 1, 1, 2, p, None, None) == 1
+    # rowcopy: rows not a multiple of 16, K not a multiple of 64 or past 16384, buffers too small
+    assert lib.vxf_rowcopy(p, 1 << 30, 17, 4096, p, 1 << 30, None) == 1
+    assert lib.vxf_rowcopy(p, 1 << 30, 16, 4100, p, 1 << 30, None) == 1
+    assert lib.vxf_rowcopy(p, 1 << 30, 16, 32768, p, 1 << 30, None) == 1
+    assert lib.vxf_rowcopy(p, 1000, 16, 4096, p, 1 << 30, None) == 1
+    assert lib.vxf_rowcopy(p, 1 << 30, 16, 4096, p, 1000, None) == 1

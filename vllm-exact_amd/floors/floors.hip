@@ -15,6 +15,8 @@
 //   mfma_shape  the two INT8 MFMA shapes at equal work per round (16x16x64 on 8 accumulators,
 //            32x32x32 on 4), their operands the same in every instruction or drawn at random
 //            with a different set in every instruction (as a GEMM's digit fragments are)
+//   rowcopy  the packed digitize's grid and traffic with no arithmetic: a workgroup per row,
+//            each lane copying 16 bf16 columns into 16-byte pieces of the two digit planes
 //   mfma_mix MFMAs and loads (L2-resident, or L2 and HBM) at once, in the large-M exact GEMM's
 //            proportion, with the shader clock each workgroup ran at
 //
@@ -256,6 +258,23 @@ __global__ __launch_bounds__(512) void mfma_shape_kernel(int rounds, int* sink, 
   finish(sink, cycles, acc, t0);
 }
 
+// One workgroup per row r (rows spread so that the 16 rows of a packed tile run on one XCD, as
+// the digitize kernel spreads them), K/16 lanes; lane c reads columns [16c, 16c + 16) of its
+// row (32 bytes) and writes 16 bytes into each of the two 1 KiB digit planes of the packed
+// fragment-major layout, where the digitize kernel writes that chunk's digits.
+__global__ __launch_bounds__(1024) void rowcopy_kernel(const uint16_t* __restrict__ x, int64_t K,
+                                                       int8_t* __restrict__ h, int64_t KT) {
+  const int64_t lin = blockIdx.x, total = gridDim.x;
+  const int64_t xcd = lin % 8, j = lin / 8, base = total / 8, rem = total % 8;
+  const int64_t row = xcd * base + (xcd < rem ? xcd : rem) + j;
+  const int64_t c = threadIdx.x;
+  const uint4* src = reinterpret_cast<const uint4*>(x + row * K + c * 16);
+  const uint4 a = src[0], b = src[1];
+  int8_t* dst = h + ((row >> 4) * KT + (c >> 2)) * 2048 + ((int)(c & 3) * 16 + (int)(row & 15)) * 16;
+  *reinterpret_cast<uint4*>(dst) = a;
+  *reinterpret_cast<uint4*>(dst + 1024) = b;
+}
+
 // MFMAs and loads together, the mix of the large-M exact GEMM: 8 waves per workgroup, one
 // workgroup per CU. Each round a wave issues eight 16-byte loads per lane (8 KiB) when
 // loads > 0: all from the L2-resident buffer `l2` (offsets masked into it), or with loads == 2
@@ -440,6 +459,17 @@ int vxf_mfma_mix(const void* l2, int64_t l2_bytes, const void* hbm, int64_t hbm_
   hipLaunchKernelGGL(mfma_mix_kernel, dim3(blocks), dim3(512), 0, (hipStream_t)stream, (const v4i*)l2,
                      l2_bytes / 16 - 1, (const v4i*)hbm, chunk ? chunk / 16 - 1 : 0, loads, mfmas, vary, rounds, sink,
                      clk);
+  return hipGetLastError() == hipSuccess ? 0 : 4;
+}
+
+// rowcopy: rows a positive multiple of 16, K a multiple of 64 with K / 16 lanes in 64 .. 1024,
+// x holding rows * K bf16 and h rows * K * 2 bytes.
+int vxf_rowcopy(const void* x, int64_t x_bytes, int64_t rows, int64_t k, void* h, int64_t h_bytes, void* stream) {
+  if (!x || !h || rows <= 0 || rows % 16 || k % 64 || k / 16 < 64 || k / 16 > 1024 || x_bytes < rows * k * 2 ||
+      h_bytes < rows * k * 2 || rows > 0x7FFFFFFFLL)
+    return 1;
+  hipLaunchKernelGGL(rowcopy_kernel, dim3((unsigned)rows), dim3((unsigned)(k / 16)), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, k, (int8_t*)h, k / 64);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
