@@ -435,6 +435,8 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
       const int i = r * C + c;
       const int64_t c0 = (wave + (int64_t)NWK * i) * 64 + kq * 16;  // this lane's first column
       if (wave + (int64_t)NWK * i < nsteps) {
+        // columns of this lane's 16 inside K (all 16 but in the chunk K ends in)
+        const int lim = (int)min<int64_t>(p.K - c0, 16);
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -446,13 +448,12 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
             int32_t hd, ld;
             if constexpr (OFFSET) {
               // columns past K keep zero digits: the weights' padding digits are zero too, and
-              // the digitize kernels leave those columns out of the sum
-              hd = 0;
-              ld = 0;
-              if (c0 + 4 * q + b < p.K) {
-                digits_offset(v, scale, hd, ld);
-                cs += (uint32_t)(256 * hd + ld);
-              }
+              // the digitize kernels leave those columns out of the sum (a select, not a branch)
+              digits_offset(v, scale, hd, ld);
+              const bool in_k = 4 * q + b < lim;
+              hd = in_k ? hd : 0;
+              ld = in_k ? ld : 0;
+              cs += (uint32_t)(256 * hd + ld);
             } else {
               digits_balanced(v, scale, hd, ld);
             }
