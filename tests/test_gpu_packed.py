@@ -138,9 +138,10 @@ def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
     """exact_linear_bf16x (x digitized inside the GEMM launch, each workgroup its own 16 rows)
     gives the oracle's bits for every one-row-tile config, with ragged M, N and K (K not a
     multiple of 64, 16 or 8), rows of magnitudes 1e-3 to 1e3 and a zero row; the
-    exactmm::linear op takes this path and gives the same bits. F = 15 (offset digits, with
-    the row digit sums in the epilogue) runs in one launch only on the x-in-registers kernel:
-    the cfgs it declines raise NotImplementedError, and those it takes must match too."""
+    exactmm::linear op takes this path and gives the same bits. F = 15 (offset digits, 4 dots,
+    the row digit sums in the epilogue) runs in one launch on both kernels, x in registers and
+    the row pass; it declines (NotImplementedError) only the 16-wave shapes with four column
+    tiles times steps per round, whose digit sum would spill, and what it takes must match."""
     x, w = stress_xw(M, N, Kd, seed=M * 7 + Kd)
     x = (x * (10.0 ** torch.linspace(-3, 3, M))[:, None]).to(torch.bfloat16)
     if M >= 3:
@@ -156,12 +157,11 @@ def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
         try:
             y = K.exact_linear_bf16x(xg, wp, Kd, F, tr, cfg=cfg)
         except NotImplementedError:
-            assert F == 15, cfg
+            assert F == 15 and cfg[3] == 16 and cfg[1] // 16 * cfg[4] >= 4, cfg
             continue
         taken.append(cfg)
         assert np.array_equal(f32_bits(y.cpu().numpy()), f32_bits(ref32)), cfg
-    fits = Kd <= 4096 and N <= 256 * 16  # F = 15: some register-path shape covers these
-    assert taken if (F < 15 or fits) else True
+    assert taken
     want_b = oracle.bf16_rne_c(ref32).reshape(M, N)
     if taken:
         yb = torch.empty(M, N + 8, device=DEV, dtype=torch.bfloat16)[:, :N]  # row stride N + 8
@@ -178,9 +178,9 @@ def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
 
 
 def test_fused_path_declines_and_the_op_falls_back():
-    """Where one launch does not apply (F = 15, x rows not 16-byte aligned, a split-K or
-    wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's two-launch path
-    still gives the oracle's bits."""
+    """Where one launch does not apply (x rows not 16-byte aligned, at F = 14 and 15; a split-K
+    or wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's two-launch
+    path still gives the oracle's bits."""
     g = torch.Generator().manual_seed(5)
     N, Kd = 96, 1001  # K = 1001: bf16 rows of 2002 bytes, not 16-byte aligned
     w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)

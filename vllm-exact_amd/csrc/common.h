@@ -76,6 +76,22 @@ __device__ inline void digits_offset(float v, float scale, int32_t& hd, int32_t&
   hd = (int32_t)(uq - (uint32_t)ld - 128u) >> 8;
 }
 
+// The packed digit words of four values q_j = trunc(v_j * scale), as the MFMA operands take
+// them: byte j of h4 / l4 is the low byte of q_j's high / low digit, the bytes digits_balanced
+// and digits_offset give. Balanced digits (F < 15): high = byte 1 of q + 128, low = byte 0 of
+// q + 128 with its top bit flipped. Offset digits (F == 15): high = byte 1 of q, low = byte 0
+// of q with its top bit flipped (q = 128 gives zero digits). Four byte permutes and one xor.
+template <bool OFFSET>
+__device__ inline void pack_digit_bytes(const int32_t (&q)[4], uint32_t& h4, uint32_t& l4) {
+  uint32_t y[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) y[j] = OFFSET ? (uint32_t)q[j] : (uint32_t)q[j] + 128u;
+  const uint32_t p01 = __builtin_amdgcn_perm(y[1], y[0], 0x05040100u);  // y0.b0 y0.b1 y1.b0 y1.b1
+  const uint32_t p23 = __builtin_amdgcn_perm(y[3], y[2], 0x05040100u);  // y2.b0 y2.b1 y3.b0 y3.b1
+  l4 = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+  h4 = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+}
+
 // Workgroups are handed to the 8 XCDs round-robin (linear id % 8), and each XCD has its own
 // L2. This bijection gives XCD x the logical ids [x*base + min(x, rem), ...) in dispatch
 // order, so neighbouring logical tiles (which share an operand tile) run on one XCD at about

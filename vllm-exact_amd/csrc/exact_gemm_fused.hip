@@ -31,8 +31,11 @@ struct FusedParams {
 };
 
 // FEW: M <= 4, one tile of at most 4 rows (decode); its row pass is the only one compiled in.
-template <int NT, int NWK, int C, bool TRUNC, bool FEW>
+// OFFSET (F = 15, 4 dots): offset digits, each row's digit sum cx added in the epilogue
+// (kernels.py:31-34, 96-97), as in the x-in-registers kernel below.
+template <int NT, int NWK, int C, bool TRUNC, bool FEW, bool OFFSET>
 __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
+  static_assert(!(OFFSET && TRUNC), "offset digits run 4 dots");
   constexpr int BN = 16 * NT;
   constexpr int RPW = (16 + NWK - 1) / NWK;  // tile rows each wave reduces in the row pass
   constexpr int PB = 8;                      // row-pass loads per lane in flight (full tiles)
@@ -40,6 +43,7 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
   __shared__ float s_scale[16];
   __shared__ int32_t s_sh[16];
   __shared__ float s_max[NWK][4];
+  __shared__ uint32_t s_cs[OFFSET ? NWK : 1][16];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -75,9 +79,12 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
       r[1] = uint4{0u, 0u, 0u, 0u};
     }
   };
+  uint32_t cs = 0;  // this lane's part of its row's digit sum (F = 15; wraps like the digitize kernels)
   auto x_digits = [&](int64_t s, const uint4 (&r)[2], v4i& ah, v4i& al) {
     float v[16];
     const int64_t c0 = s * 64 + kq * 16;
+    // columns of this lane's 16 inside K (all 16 but in the chunk K ends in; none past it)
+    const int lim = (int)max<int64_t>(min<int64_t>(p.K - c0, 16), 0);
     if (!row_ok || c0 + 16 <= p.K) {
       const uint32_t w[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
 #pragma unroll
@@ -92,16 +99,18 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      uint32_t h4 = 0, l4 = 0;
+      int32_t qv[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        int32_t hd, ld;
-        digits_balanced(v[4 * q + b], scale, hd, ld);
-        h4 |= ((uint32_t)hd & 255u) << (8 * b);
-        l4 |= ((uint32_t)ld & 255u) << (8 * b);
+        qv[b] = (int32_t)(v[4 * q + b] * scale);  // truncation toward zero
+        if constexpr (OFFSET) {
+          // columns past K keep zero digits and stay out of the sum, as in the digitize kernels:
+          // q = 128 is zero offset digits, and the sum adds 256 h + l = q - 128
+          qv[b] = 4 * q + b < lim ? qv[b] : 128;
+          cs += (uint32_t)qv[b] - 128u;
+        }
       }
-      hw[q] = h4;
-      lw[q] = l4;
+      pack_digit_bytes<OFFSET>(qv, hw[q], lw[q]);
     }
     ah = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
     al = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
@@ -286,7 +295,13 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
     }
   }
 
-  // 3. Wave partials meet in LDS (exact int64 adds), then the epilogue.
+  // 3. Wave partials meet in LDS (exact int64 adds), then the epilogue; with offset digits the
+  // row sums meet too (the row's 4 lanes, then the waves, all mod 2^32).
+  if constexpr (OFFSET) {
+    cs += __shfl_xor(cs, 16);
+    cs += __shfl_xor(cs, 32);
+    if (kq == 0) s_cs[wave][r16] = cs;
+  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -302,8 +317,16 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_kernel(FusedParams p) {
   for (int i = threadIdx.x; i < mrows * BN; i += nthr) {
     const int m = i / BN;
     const int64_t n = n0 + i % BN;
-    if (n < p.N)
-      store_f32_as(p.out, p.out_dtype, (m0 + m) * p.ldo + n, exact_epilogue((int64_t)red[i], s_sh[m], p.sw[n]));
+    if (n < p.N) {
+      int64_t tot = (int64_t)red[i];
+      if constexpr (OFFSET) {  // 128 (cx + cw) + 128^2 K (kernels.py:96-97, 148-151)
+        uint32_t cx = 0;
+#pragma unroll
+        for (int w = 0; w < NWK; ++w) cx += s_cs[w][m];
+        tot += 128 * ((int64_t)(int32_t)cx + (int64_t)p.cw[n]) + 128 * 128 * p.K;
+      }
+      store_f32_as(p.out, p.out_dtype, (m0 + m) * p.ldo + n, exact_epilogue(tot, s_sh[m], p.sw[n]));
+    }
   }
 }
 
@@ -440,28 +463,21 @@ __global__ __launch_bounds__(64 * NWK) void exact_fused_xreg_kernel(FusedParams 
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          uint32_t h4 = 0, l4 = 0;
+          int32_t qv[4];
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
             const uint32_t w = xw[i][(4 * q + b) >> 1];
             const float v = __uint_as_float(((4 * q + b) & 1) ? (w & 0xFFFF0000u) : (w << 16));
-            int32_t hd, ld;
+            qv[b] = (int32_t)(v * scale);  // truncation toward zero
             if constexpr (OFFSET) {
               // columns past K keep zero digits: the weights' padding digits are zero too, and
-              // the digitize kernels leave those columns out of the sum (a select, not a branch)
-              digits_offset(v, scale, hd, ld);
-              const bool in_k = 4 * q + b < lim;
-              hd = in_k ? hd : 0;
-              ld = in_k ? ld : 0;
-              cs += (uint32_t)(256 * hd + ld);
-            } else {
-              digits_balanced(v, scale, hd, ld);
+              // the digitize kernels leave those columns out of the sum (a select, not a branch;
+              // q = 128 is zero offset digits, and the sum adds 256 h + l = q - 128)
+              qv[b] = 4 * q + b < lim ? qv[b] : 128;
+              cs += (uint32_t)qv[b] - 128u;
             }
-            h4 |= ((uint32_t)hd & 255u) << (8 * b);
-            l4 |= ((uint32_t)ld & 255u) << (8 * b);
           }
-          hw[q] = h4;
-          lw[q] = l4;
+          pack_digit_bytes<OFFSET>(qv, hw[q], lw[q]);
         }
         const v4i ah = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
         const v4i al = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
@@ -532,6 +548,13 @@ constexpr bool xreg_fits() {
   return XS == 8 && NWK <= 8 && (NT * C <= 2 || (NT == 4 && C == 1 && TRUNC && !OFFSET));
 }
 
+// Row-pass shapes whose offset-digit (F = 15) instantiation compiles without scratch (gfx950
+// -O3): with 16 waves (128 VGPRs a lane) at most two column tiles times steps per round.
+template <int NT, int NWK, int C>
+constexpr bool rowpass_offset_fits() {
+  return NWK < 16 || NT * C < 4;
+}
+
 // Compute units of the current device (cached per device; 0 when the query fails).
 int device_cus() {
   static int cus[64] = {};
@@ -564,14 +587,19 @@ hipError_t launch(const FusedParams& fp, hipStream_t st) {
   }
   VXA_XREG(4, false) VXA_XREG(8, false) VXA_XREG(4, true) VXA_XREG(8, true)
 #undef VXA_XREG
-  if (fp.F == 15) return hipErrorInvalidValue;  // offset digits: the register path only
-  if (fp.M <= 4)
-    hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, true>), dim3((unsigned)blocks), dim3(64 * NWK), 0, st,
-                       fp);
-  else
-    hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, false>), dim3((unsigned)blocks), dim3(64 * NWK), 0,
-                       st, fp);
-  return hipGetLastError();
+  // the row-pass kernel: balanced digits, or offset digits (F = 15) with 4 dots
+#define VXA_ROWPASS(FEW_, OFF_)                                                                                   \
+  if ((fp.M <= 4) == FEW_ && (fp.F == 15) == OFF_) {                                                             \
+    hipLaunchKernelGGL((exact_fused_kernel<NT, NWK, C, TRUNC, FEW_, OFF_>), dim3((unsigned)blocks), dim3(64 * NWK), \
+                       0, st, fp);                                                                               \
+    return hipGetLastError();                                                                                    \
+  }
+  VXA_ROWPASS(true, false) VXA_ROWPASS(false, false)
+  if constexpr (!TRUNC && rowpass_offset_fits<NT, NWK, C>()) {
+    VXA_ROWPASS(true, true) VXA_ROWPASS(false, true)
+  }
+#undef VXA_ROWPASS
+  return hipErrorInvalidValue;  // offset digits with 3 dots, or a shape whose digit sum would spill
 }
 
 // (NT, C, NWK): the small-M kernel's one-row-tile shapes.
