@@ -60,27 +60,16 @@ __device__ inline float digit_scale(float absmax, int F, int& sh) {
   return __uint_as_float((uint32_t)(sh + 127) << 23);
 }
 
-// Balanced digits (F < 15, kernels.py:35-38) of q = trunc(v * scale): q = 256 h + l with
-// l in [-128, 127].
-__device__ inline void digits_balanced(float v, float scale, int32_t& hd, int32_t& ld) {
-  const uint32_t uq = (uint32_t)(int32_t)(v * scale);  // truncation toward zero
-  ld = (int32_t)((uq + 128u) & 255u) - 128;
-  hd = (int32_t)(uq - (uint32_t)ld) >> 8;
-}
-
-// Offset digits (F == 15, kernels.py:31-34) of q = trunc(v * scale): q = 256 h + l + 128 with
-// l in [-128, 127], in 32-bit wrap-around arithmetic.
-__device__ inline void digits_offset(float v, float scale, int32_t& hd, int32_t& ld) {
-  const uint32_t uq = (uint32_t)(int32_t)(v * scale);  // truncation toward zero
-  ld = (int32_t)(uq & 255u) - 128;
-  hd = (int32_t)(uq - (uint32_t)ld - 128u) >> 8;
-}
-
 // The packed digit words of four values q_j = trunc(v_j * scale), as the MFMA operands take
-// them: byte j of h4 / l4 is the low byte of q_j's high / low digit, the bytes digits_balanced
-// and digits_offset give. Balanced digits (F < 15): high = byte 1 of q + 128, low = byte 0 of
-// q + 128 with its top bit flipped. Offset digits (F == 15): high = byte 1 of q, low = byte 0
-// of q with its top bit flipped (q = 128 gives zero digits). Four byte permutes and one xor.
+// them: byte j of h4 / l4 is the low byte of q_j's high / low digit.
+//   Balanced digits (F < 15, kernels.py:35-38): q = 256 h + l, l in [-128, 127], so
+//   l = ((q + 128) & 255) - 128 and h = (q - l) >> 8: h's byte is byte 1 of q + 128 and l's
+//   byte 0 of q + 128 with its top bit flipped.
+//   Offset digits (F == 15, kernels.py:31-34): q = 256 h + l + 128 in 32-bit wrap-around
+//   arithmetic, so l = (q & 255) - 128 and h = (q - l - 128) >> 8: h's byte is byte 1 of q and
+//   l's byte 0 of q with its top bit flipped; 256 h + l = q - 128, and q = 128 gives zero
+//   digits.
+// Four byte permutes and one xor.
 template <bool OFFSET>
 __device__ inline void pack_digit_bytes(const int32_t (&q)[4], uint32_t& h4, uint32_t& l4) {
   uint32_t y[4];

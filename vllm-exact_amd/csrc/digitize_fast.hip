@@ -141,35 +141,39 @@ __global__ __launch_bounds__(kMaxThreads) void digitize_fast_kernel(const void* 
   for (int i = 0; i < CPT; ++i) {
     const int64_t c = threadIdx.x + (int64_t)i * nthr;
     if (c >= nchunk) continue;
-    uint8_t hb[16], lb[16];
+    // Digit bytes straight from q = trunc(v * scale) (pack_digit_bytes). Columns past K: v is
+    // zero, so balanced digits are zero; offset digits take q = 128 (zero digits, and nothing
+    // added to the sum, which adds 256 h + l = q - 128 per column).
+    const int lim = (int)max<int64_t>(min<int64_t>(K - c * 16, 16), 0);
+    uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      int32_t hd = 0, ld = 0;
-      if (c * 16 + j < K) {
+    for (int g = 0; g < 4; ++g) {
+      int32_t qv[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        qv[b] = (int32_t)(v[i][4 * g + b] * scale);  // truncation toward zero
         if constexpr (OFFSET) {
-          digits_offset(v[i][j], scale, hd, ld);
-          csum += (uint32_t)(256 * hd + ld);
-        } else {
-          digits_balanced(v[i][j], scale, hd, ld);
+          qv[b] = 4 * g + b < lim ? qv[b] : 128;
+          csum += (uint32_t)qv[b] - 128u;
         }
       }
-      hb[j] = (uint8_t)hd;
-      lb[j] = (uint8_t)ld;
+      pack_digit_bytes<OFFSET>(qv, hw[g], lw[g]);
     }
+    const uint4 hv = uint4{hw[0], hw[1], hw[2], hw[3]}, lv = uint4{lw[0], lw[1], lw[2], lw[3]};
     if constexpr (PACKED) {
       int8_t* dst = h + ((row >> 4) * KT + (c >> 2)) * 2048 + ((int)(c & 3) * 16 + (int)(row & 15)) * 16;
-      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(hb);
-      *reinterpret_cast<uint4*>(dst + 1024) = *reinterpret_cast<const uint4*>(lb);
+      *reinterpret_cast<uint4*>(dst) = hv;
+      *reinterpret_cast<uint4*>(dst + 1024) = lv;
     } else {
       int8_t* hr = h + row * ldd + c * 16;
       int8_t* lr = l + row * ldd + c * 16;
       if (vec && c * 16 + 16 <= K) {
-        *reinterpret_cast<uint4*>(hr) = *reinterpret_cast<const uint4*>(hb);
-        *reinterpret_cast<uint4*>(lr) = *reinterpret_cast<const uint4*>(lb);
+        *reinterpret_cast<uint4*>(hr) = hv;
+        *reinterpret_cast<uint4*>(lr) = lv;
       } else {
-        for (int j = 0; j < 16 && c * 16 + j < K; ++j) {
-          hr[j] = (int8_t)hb[j];
-          lr[j] = (int8_t)lb[j];
+        for (int j = 0; j < lim; ++j) {
+          hr[j] = (int8_t)(hw[j >> 2] >> (8 * (j & 3)));
+          lr[j] = (int8_t)(lw[j >> 2] >> (8 * (j & 3)));
         }
       }
     }

@@ -8,7 +8,7 @@
 //      one wave per row, each lane's loads batched so a row costs one or two L2 round trips)
 //      gives each row's scale (digit_scale, the digitize kernels' own helper);
 //   2. in the K loop, a lane reads its 16 bf16 columns of its row straight from x and splits
-//      them into the two MFMA digit operands (digits_balanced) in registers;
+//      them into the two MFMA digit operands (pack_digit_bytes) in registers;
 //   3. MFMAs, wave partials and the epilogue are the small-M kernel's (exact_gemm_sm.hip).
 // The digits are the ones the digitize kernel writes, so every output bit is the two-launch
 // path's. Lanes of rows past M take zero operands; their results are never stored.
