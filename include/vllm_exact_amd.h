@@ -132,9 +132,9 @@ int vxa_exact_linear_packed(const int8_t* xp, const int32_t* cx, const int32_t* 
  *        plan keeps one K split (int32 digit sums stay exact)
  * Each workgroup digitizes its own 16 rows of x (row absmax over k, then the digits in
  * registers). Returns VXA_ERR_UNSUPPORTED for another cfg family, a plan with more than one
- * K split, x rows that are not 16-byte aligned, or f = 15 where its x-in-registers kernel
- * does not apply (more workgroups than CUs, a K longer than its registers hold, 3 dots): the
- * caller then takes the two-launch path. No reference counterpart:
+ * K split, x rows that are not 16-byte aligned, or f = 15 with 3 dots or on a 16-wave cfg
+ * with four column tiles times steps per round (whose digit sum would spill): the caller
+ * then takes the two-launch path. No reference counterpart:
  * the reference digitizes x in a launch of its own (plugin.py:62-64); this entry point serves
  * the exactmm::linear op at decode sizes, where that launch is a quarter of the op.
  */
