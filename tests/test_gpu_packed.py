@@ -177,6 +177,44 @@ def test_fused_digitize_gemm_bitwise(F, tr, M, N, Kd):
         assert np.array_equal(y_op.cpu().view(torch.int16).numpy().view(np.uint16), want_b)
 
 
+def test_random_shapes_one_and_two_launch_bitwise():
+    """A seeded sweep of 160 random cases (M 1-64, N 1-900, K 8-12288 including K not a
+    multiple of 16 or 64, F = 12 / 14 / 15 with and without truncation, rows scaled by 1e-3 to
+    1e3): a random one-row-tile cfg on the one-launch path and a random packed cfg and split-K
+    factor on the two-launch path, both equal to the oracle bit for bit. The one-launch path
+    declines only the F = 15 16-wave cfgs with four column tiles times steps per round."""
+    import random
+
+    rng = random.Random(1234)
+    n_taken = 0
+    for case in range(160):
+        M = rng.choice([1, 2, 3, 4, 5, 8, 13, 16, 17, 31, 40, 64])
+        N = rng.randint(1, 900)
+        Kd = rng.choice([8, 16, 40, 64, 72, 128, 520, 1000, 2048, 4096, 4104, 8192, 12288])
+        F, tr = rng.choice([(14, True), (14, False), (12, True), (15, False)])
+        cfg = rng.choice(FUSED_CFGS)
+        cfg2 = rng.choice(PACKED_CFGS) + (rng.choice([1, 2, 4, 8]),)
+        x, w = stress_xw(M, N, Kd, seed=case)
+        scale = 10.0 ** torch.empty(M).uniform_(-3, 3, generator=torch.Generator().manual_seed(case))
+        x = (x * scale[:, None]).to(torch.bfloat16)
+        wb = w.to(torch.bfloat16)
+        ref = f32_bits(oracle.exact_linear_c(oracle.digitize_c(x.float().numpy(), F),
+                                             oracle.digitize_c(wb.float().numpy(), F), F, tr))
+        wp = K.digitize_packed(wb.to(DEV), F)
+        xg = x.to(DEV)
+        what = (case, M, N, Kd, F, tr)
+        try:
+            y = K.exact_linear_bf16x(xg, wp, Kd, F, tr, cfg=cfg)
+        except NotImplementedError:
+            assert F == 15 and cfg[3] == 16 and cfg[1] // 16 * cfg[4] >= 4, what + (cfg,)
+        else:
+            assert np.array_equal(f32_bits(y.cpu().numpy()), ref), what + (cfg,)
+            n_taken += 1
+        y2 = K.exact_linear_packed(K.digitize_packed(xg, F), wp, Kd, F, tr, cfg=cfg2)
+        assert np.array_equal(f32_bits(y2.cpu().numpy()), ref), what + (cfg2,)
+    assert n_taken >= 140
+
+
 def test_fused_path_declines_and_the_op_falls_back():
     """Where one launch does not apply (x rows not 16-byte aligned, at F = 14 and 15; a split-K
     or wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's two-launch

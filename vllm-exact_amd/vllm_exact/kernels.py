@@ -218,9 +218,9 @@ def exact_linear_bf16x(x, wp, K, F, trunc=False, out=None, cfg=None):
     """Digitize x (bf16 [M, K]) and run exact_linear_packed in one launch: the bits of
     exact_linear_packed(digitize_packed(x, F), wp, K, F, trunc, cfg=cfg). Raises
     NotImplementedError where the one-launch path does not apply (a cfg outside the
-    one-row-tile small-M family or with split-K, x rows not 16-byte aligned, or F = 15 where
-    its x-in-registers kernel does not: 3 dots, more workgroups than CUs, K beyond its
-    registers); the two-launch path covers those."""
+    one-row-tile small-M family or with split-K, x rows not 16-byte aligned, or F = 15 with
+    3 dots or on a 16-wave cfg with four column tiles times steps per round, whose digit sum
+    would spill); the two-launch path covers those."""
     pw, cw, sw = wp
     _require_gpu(x, "exact_linear_bf16x")
     if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
