@@ -237,3 +237,38 @@ def test_head_dims_and_groups(D, H, KV):
     o = _run(q, kv, bt, sl, D ** -0.5, 5, D)
     want = _oracle(q, kv, bt, sl, D ** -0.5, 5, D)
     _check_tol(o.cpu().numpy(), want)
+
+
+def test_random_shapes_against_the_oracle():
+    """A seeded sweep of 30 random cases over what the kernel accepts: head dims 64 / 128 / 256,
+    groups 1 / 2 / 4 / 8 (H <= 32), page sizes 8 / 16 / 32 / 528, 1-6 requests of 1-3000 keys,
+    (blk, waves, split) from {16, 32, 64} x {4, 8} x {512, 1024, 2048}, fp32 and bf16 output.
+    Every request is within the stated tolerance of the float64 oracle, and one random request
+    run alone gives the bits it gets in the batch."""
+    import random
+
+    rng = random.Random(4321)
+    for case in range(30):
+        D = rng.choice([64, 128, 256])
+        KV = rng.choice([1, 2, 4, 8])
+        G = rng.choice([g for g in (1, 2, 4, 8) if g * KV <= 32])
+        BS = rng.choice([8, 16, 32, 528])
+        B, L = rng.randint(1, 6), rng.randint(1, 3000)
+        blk, waves, split = rng.choice([16, 32, 64]), rng.choice([4, 8]), rng.choice([512, 1024, 2048])
+        out_dtype = rng.choice([torch.float32, torch.bfloat16])
+        scale = D ** -0.5 * rng.uniform(0.5, 1.5)
+        what = (case, D, G * KV, KV, BS, B, L, blk, waves, split, out_dtype)
+        print(what, flush=True)
+        q, kv, bt, sl = make_paged(B, L, BS, G * KV, KV, D, seed=case, var_len=L > 1)
+        q, kv, bt, sl = q.to(DEV), kv.to(DEV), bt.to(DEV), sl.to(DEV)
+        kw = dict(blk=blk, warps=waves, split=split)
+        o = _run(q, kv, bt, sl, scale, B, D, out_dtype, **kw)
+        want = _oracle(q, kv, bt, sl, scale, B, D)
+        got = o.float().cpu().numpy()
+        if out_dtype == torch.float32:
+            _check_tol(got, want)
+        else:
+            _check_tol_bf16(got, want)
+        b = rng.randrange(B)
+        alone = _run(q[b:b + 1], kv, bt[b:b + 1], sl[b:b + 1], scale, 1, D, out_dtype, **kw)
+        assert torch.equal(alone[0], o[b]), what
