@@ -4,7 +4,8 @@
   weights, with the shipped F = 14 table (3 dots) and F = 15 table (offset digits, 4 dots),
   at 16 and 256 rows with per-row activation scales 10^U(-2, 2): every column of sampled rows
   against the oracle;
-* the F = 15 table through the op at the four decode-sweep shapes and 1-256 rows;
+* the F = 15 table through the op at the four decode-sweep shapes and 1-256 rows, and both
+  tables at seeded random batch sizes of 1-512 rows;
 * autotune_exact, the reference's path when no cfg is given (kernels.py:267, 292-316);
 * the vLLM plugin hooks process_weights_after_loading and apply (plugin.py:87-102), run on
   stand-in vLLM base classes, with a bias and with the lm_head.
@@ -107,6 +108,32 @@ def test_f15_table_through_the_op_at_sweep_shapes(monkeypatch, N, Kd):
         want = oracle.bf16_rne_c(oracle.exact_linear_c(xd_np, wd_np, 15, False)).reshape(len(rows), N)
         assert np.array_equal(bf16_bits(y)[rows], want), (M, N, Kd, plugin._cfg(M, N, Kd),
                                                           plugin._one_launch(M, N, Kd))
+
+
+@pytest.mark.parametrize("F", [14, 15])
+def test_both_tables_through_the_op_at_random_batch_sizes(monkeypatch, F):
+    """The shipped F = 14 and F = 15 tables through the op at the four decode-sweep shapes, at
+    seeded random batch sizes of 1-512 rows (most between the table's buckets, so the lookup
+    picks a neighbouring bucket's cfg and, below 17 rows, the one- or two-launch path): the
+    first, two random and the last row equal the oracle's bf16 bits."""
+    import random
+
+    use(monkeypatch, F)
+    rng = random.Random(F)
+    g = torch.Generator().manual_seed(F)
+    for N, Kd in SWEEP:
+        w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)
+        wbuf = plugin.pack_weight(w.to(DEV))
+        wd_np = oracle.digitize_c(w.float().numpy(), F)
+        for M in sorted(rng.sample(range(1, 513), 4)):
+            x = torch.randn(M, Kd, generator=g) * (10.0 ** torch.empty(M, 1).uniform_(-2, 2, generator=g))
+            x = x.to(torch.bfloat16)
+            y = torch.ops.exactmm.linear(x.to(DEV), *wbuf)
+            rows = np.unique(np.array([0, rng.randrange(M), rng.randrange(M), M - 1]))
+            xd_np = oracle.digitize_c(x.float().numpy()[rows], F)
+            want = oracle.bf16_rne_c(oracle.exact_linear_c(xd_np, wd_np, F, F == 14)).reshape(len(rows), N)
+            assert np.array_equal(bf16_bits(y)[rows], want), (F, M, N, Kd, plugin._cfg(M, N, Kd),
+                                                              plugin._one_launch(M, N, Kd))
 
 
 @pytest.mark.parametrize("M,N,Kd", [(16, 512, 1024), (37, 200, 1000)])
