@@ -215,6 +215,49 @@ def test_random_shapes_one_and_two_launch_bitwise():
     assert n_taken >= 140
 
 
+@pytest.mark.parametrize("F,tr", [(14, True), (15, False), (12, True)])
+def test_rows_at_the_edge_of_the_scale_exponent(F, tr):
+    """Rows so small that 2^sh, built from exponent bits, leaves the float range: shifts
+    124 ... 133 around sh = 128 (the scale is +inf there, x * scale is +-inf, and
+    NaN where x = 0; beyond it the exponent field wraps) and bf16 subnormal rows, with zeros
+    and both signs in every row. float -> int32 saturates with NaN -> 0, as the device cast
+    does (oracle trunc_i32). Digits and shifts from fp32 and bf16 input, packed digits, and
+    both GEMM paths equal the oracle bit for bit."""
+    g = torch.Generator().manual_seed(F)
+    Kd, N = 200, 48
+    exps = [F - 1 - sh for sh in range(124, 134)] + [-126, -130, -133]  # absmax 2^e: sh = F - e - 1
+    x = torch.randn(len(exps) + 1, Kd, generator=g)
+    x[:, ::7] = 0
+    x = x / x.abs().amax(dim=1, keepdim=True)
+    x[:len(exps)] *= torch.tensor([2.0 ** e for e in exps])[:, None]
+    xb = x.to(torch.bfloat16)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).to(torch.bfloat16)
+    for src in (x, xb.float()):
+        want = oracle.digitize_c(src.numpy(), F)
+        got = np_digits(K.digitize(src.to(DEV), F))
+        for a, b, name in zip(got, want, ("h", "l", "cs", "sh")):
+            assert np.array_equal(a, b), name
+    xd_np = oracle.digitize_c(xb.float().numpy(), F)
+    assert xd_np[3][:10].tolist() == list(range(124, 134))
+    px, pcx, psx = K.digitize_packed(xb.to(DEV), F)
+    assert np.array_equal(px.cpu().numpy(), pack_np(xd_np[0], xd_np[1]))
+    assert np.array_equal(pcx.cpu().numpy(), xd_np[2]) and np.array_equal(psx.cpu().numpy(), xd_np[3])
+    ref = f32_bits(oracle.exact_linear_c(xd_np, oracle.digitize_c(w.float().numpy(), F), F, tr))
+    wp = K.digitize_packed(w.to(DEV), F)
+    y = K.exact_linear_packed((px, pcx, psx), wp, Kd, F, tr, cfg=(16, 64, 128, 4, 1, 8, 1))
+    assert np.array_equal(f32_bits(y.cpu().numpy()), ref)
+    taken = 0
+    for cfg in FUSED_CFGS:
+        try:
+            y = K.exact_linear_bf16x(xb.to(DEV), wp, Kd, F, tr, cfg=cfg)
+        except NotImplementedError:
+            assert F == 15 and cfg[3] == 16 and cfg[1] // 16 * cfg[4] >= 4, cfg
+            continue
+        taken += 1
+        assert np.array_equal(f32_bits(y.cpu().numpy()), ref), cfg
+    assert taken
+
+
 def test_fused_path_declines_and_the_op_falls_back():
     """Where one launch does not apply (x rows not 16-byte aligned, at F = 14 and 15; a split-K
     or wide-tile cfg) exact_linear_bf16x raises NotImplementedError, and the op's two-launch
